@@ -1,0 +1,170 @@
+/*
+ * icsa.h -- C ABI of the MI355X (gfx950) in-context sparse attention library (libicsa.so).
+ *
+ * Every entry point takes raw device pointers, explicit sizes and element strides, and a
+ * HIP stream (passed as void*, 0 = the null stream).  Work is enqueued on that stream and
+ * the call returns without synchronising.  Nothing here allocates device memory: scratch
+ * comes from a caller-provided workspace whose size the matching *_workspace_size()
+ * function returns.  Results are deterministic (fixed reduction orders, no float atomics).
+ *
+ * Status codes: ICSA_OK (0) or a negative ICSA_E*; icsa_last_error() returns a
+ * thread-local message describing the last failure on the calling thread.
+ *
+ * Tensors: dtype codes ICSA_BF16 / ICSA_F32.  Token tensors are [B, S, H, D] (or the
+ * reference's [B, H, T, D] for the sparse host function) with the innermost dimension
+ * contiguous; strides are in elements.  Only D = 128 is supported.  Base pointers and
+ * strides must keep 16-byte alignment of every row.
+ *
+ * Reference interfaces replaced (paths relative to the reference repository root):
+ *   icsa_editing_sparse_attention   <- editing_sparse_attention(q, k, v, t_seq_len, s_seq_len,
+ *                                        alpha_2, alpha_3, SPARSITY_RATIO, backend)
+ *                                        in_context_sparse_attention/editing_sparse_attention.py:67-232
+ *   icsa_sparse_piecewise_attn      <- sparse_piecewise_attn_1st_intervals_tilelang(q, k, v,
+ *                                        sparsity, block_size)
+ *                                        in_context_sparse_attention/tilelang_host.py:229-274
+ *                                        (same contract as triton_host.py:11-30)
+ *   icsa_flash_attn                 <- flash_attn_func(q, k, v) used at
+ *                                        editing_sparse_attention.py:211-215 (third-party
+ *                                        flash-attn >= 2.7; dense non-causal attention)
+ *   icsa_pool                       <- block compression, editing_sparse_attention.py:96-111
+ *                                        and compress_seq :37-55 (sums; means = sums / size)
+ *   icsa_gather_kv                  <- new_k / new_v construction,
+ *                                        editing_sparse_attention.py:138-159
+ */
+#ifndef ICSA_H_
+#define ICSA_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ICSA_BF16 0
+#define ICSA_F32 1
+
+#define ICSA_OK 0
+#define ICSA_EINVAL (-1)       /* invalid argument (null pointer, bad shape/stride/dtype) */
+#define ICSA_EUNSUPPORTED (-2) /* valid but unsupported here (D != 128, sizes over limits) */
+#define ICSA_EWORKSPACE (-3)   /* workspace too small */
+#define ICSA_EHIP (-4)         /* HIP runtime / launch error */
+
+/* Workspace sub-buffers of icsa_editing_sparse_attention, in layout order. */
+enum icsa_ws_slot {
+  ICSA_WS_QSUM = 0,   /* f32 [B*H, NB, D]   block sums of q                       */
+  ICSA_WS_KSUM,       /* f32 [B*H, NB, D]                                          */
+  ICSA_WS_VSUM,       /* f32 [B*H, NB, D]                                          */
+  ICSA_WS_VT,         /* bf16 [B*H, D, NB*64] V transposed (kv_slot order)          */
+  ICSA_WS_QB,         /* bf16 [B, S, H, D] copy of q (only when q is f32)           */
+  ICSA_WS_KB,         /* bf16 [B, S, H, D] copy of k (only when k is f32)           */
+  ICSA_WS_P,          /* f32 [B*H, NB, NB]  compressed softmax P                    */
+  ICSA_WS_OUTC,       /* f32 [B*H, NB, D]   compressed attention output             */
+  ICSA_WS_SHARP,      /* f32 [B*H, NB]      sharpness                               */
+  ICSA_WS_SRCSCORE,   /* f32 [B*H, n_s]     source-block column mass                */
+  ICSA_WS_SEL,        /* i32 [B*H, topK]    selected source blocks (ranked)         */
+  ICSA_WS_ORDER,      /* i32 [B*H, NB]      peaked blocks then diffuse blocks        */
+  ICSA_WS_KVMAP,      /* i32 [B*H, NKV]     new-KV block -> source block (-1 zero)   */
+  ICSA_WS_KC32,       /* f32 [B*H, NKV, D]  new-KV block sums of k                   */
+  ICSA_WS_KC,         /* bf16 [B*H, NKVp, D]                                        */
+  ICSA_WS_VCT,        /* bf16 [B*H, D, NKVp] new-KV block sums of v, transposed      */
+  ICSA_WS_L3,         /* i32 [B*H, n_diffuse, top_k] per-block exact lists (ascending) */
+  ICSA_WS_KN,         /* bf16 [B*H, Tp, D]  materialised new K (t % 64 != 0 only)    */
+  ICSA_WS_VN,         /* bf16 [B*H, Tp, D]  materialised new V (t % 64 != 0 only)    */
+  ICSA_WS_VTN,        /* bf16 [B*H, D, Tp]  its transpose (t % 64 != 0 only)         */
+  ICSA_WS_NKSUM,      /* f32 [B*H, NKV, D]  (t % 64 != 0 only)                       */
+  ICSA_WS_NVSUM,      /* f32 [B*H, NKV, D]  (t % 64 != 0 only)                       */
+  ICSA_WS_COUNT
+};
+
+/* Derived sizes of one editing call (editing_sparse_attention.py:89-172,
+ * tilelang_host.py:151-171).  sizes_out[]: NB, n_t, n_s, topK, Tkv, k_sparsity,
+ * n_peaked, n_diffuse, TKV_pad, NKV, top_k, NKVp (12 entries). */
+int icsa_editing_sizes(int B, int S, int H, int D, int t_seq_len, double sparsity, double srr,
+                       double flat_ratio, int32_t* sizes_out);
+
+/* Workspace bytes of icsa_editing_sparse_attention for these shapes / dtypes. */
+int64_t icsa_editing_workspace_size(int B, int S, int H, int D, int t_seq_len, double sparsity,
+                                    double srr, double flat_ratio, int q_dtype, int k_dtype);
+
+/* Byte offsets of every ICSA_WS_* sub-buffer (offsets_out[ICSA_WS_COUNT]; size-0 slots
+ * repeat the next offset).  Returns the total size like *_workspace_size. */
+int64_t icsa_editing_workspace_layout(int B, int S, int H, int D, int t_seq_len, double sparsity,
+                                      double srr, double flat_ratio, int q_dtype, int k_dtype,
+                                      int64_t* offsets_out);
+
+/* The whole in-context sparse attention path for q, k, v [B, S, H, D] (target tokens
+ * first, t_seq_len of them): pooling, compressed attention, per-head source retrieval
+ * (SRR = srr), peaked/diffuse split (flat_ratio peaked), exact flash attention for the
+ * peaked blocks, sparse piecewise attention for the diffuse blocks, residual
+ * out = attn + alpha_2 * out_c.  q/k/v: bf16 or f32 each.  alpha: NULL -> alpha_scalar,
+ * else a tensor broadcast to [B, S, H, D] through strides (a_sd may be 0).  out: bf16 or
+ * f32 [B, S, H, D].  inject_sel [B*H, topK], inject_order [B*H, NB] and inject_l3
+ * [B*H, n_diffuse, top_k] (ascending) optionally replace the path's own decisions (NULL:
+ * computed).  s_seq_len is not needed (unused by the reference as well). */
+int icsa_editing_sparse_attention(
+    const void* q, int q_dtype, int64_t q_sb, int64_t q_ss, int64_t q_sh,
+    const void* k, int k_dtype, int64_t k_sb, int64_t k_ss, int64_t k_sh,
+    const void* v, int v_dtype, int64_t v_sb, int64_t v_ss, int64_t v_sh,
+    int B, int S, int H, int D, int t_seq_len, double sparsity, double srr, double flat_ratio,
+    const void* alpha, int alpha_dtype, int64_t a_sb, int64_t a_ss, int64_t a_sh, int64_t a_sd,
+    float alpha_scalar,
+    void* out, int out_dtype, int64_t o_sb, int64_t o_ss, int64_t o_sh,
+    const int32_t* inject_sel, const int32_t* inject_order, const int32_t* inject_l3,
+    void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Workspace bytes of icsa_sparse_piecewise_attn. */
+int64_t icsa_sparse_piecewise_workspace_size(int B, int H, int TQ, int TKV, int D, double sparsity);
+
+/* Sparse piecewise attention (first-order intervals) on q [B, H, TQ, D], k/v [B, H, TKV, D]
+ * bf16 (strides sb, sh, st), TQ and TKV multiples of 64: block sums, top_k =
+ * max(1, int(sparsity * TKV/64)) blocks per query block (inject_idx [B*H, TQ/64, top_k]
+ * ascending replaces them; idx_out receives the lists used, either may be NULL), exact
+ * attention over those blocks plus the interval approximation elsewhere.  out: bf16
+ * [B, H, TQ, D]. */
+int icsa_sparse_piecewise_attn(
+    const void* q, int64_t q_sb, int64_t q_sh, int64_t q_st,
+    const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st,
+    const void* v, int64_t v_sb, int64_t v_sh, int64_t v_st,
+    int B, int H, int TQ, int TKV, int D, double sparsity,
+    const int32_t* inject_idx, int32_t* idx_out,
+    void* out, int64_t o_sb, int64_t o_sh, int64_t o_st,
+    void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Workspace bytes of icsa_flash_attn. */
+int64_t icsa_flash_attn_workspace_size(int B, int Sk, int H, int D);
+
+/* Dense non-causal attention softmax(q k^T / sqrt(D)) v: q [B, Sq, H, D], k/v [B, Sk, H, D]
+ * bf16, out [B, Sq, H, D] bf16 or f32.  Also this library's dense baseline. */
+int icsa_flash_attn(const void* q, int64_t q_sb, int64_t q_ss, int64_t q_sh,
+                    const void* k, int64_t k_sb, int64_t k_ss, int64_t k_sh,
+                    const void* v, int64_t v_sb, int64_t v_ss, int64_t v_sh,
+                    int B, int Sq, int Sk, int H, int D,
+                    void* out, int out_dtype, int64_t o_sb, int64_t o_ss, int64_t o_sh,
+                    void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Stage 1 alone: f32 block sums [B*H, NB, D] of q, k, v [B, S, H, D] (any may be NULL)
+ * and, if vt != NULL, V transposed to bf16 [B*H, D, NB*64] (kv_slot order, zero padded). */
+int icsa_pool(const void* q, int q_dtype, int64_t q_sb, int64_t q_ss, int64_t q_sh,
+              const void* k, int k_dtype, int64_t k_sb, int64_t k_ss, int64_t k_sh,
+              const void* v, int v_dtype, int64_t v_sb, int64_t v_ss, int64_t v_sh,
+              int B, int S, int H, int D, float* qsum, float* ksum, float* vsum, void* vt,
+              void* stream);
+
+/* New-KV gather: kn, vn bf16 [B*H, Tp, D] with Tp = ceil((t + 64*topK)/64)*64 from
+ * k, v [B, S, H, D] and sel [B*H, topK] (rows past t + 64*topK are zero). */
+int icsa_gather_kv(const void* k, int k_dtype, int64_t k_sb, int64_t k_ss, int64_t k_sh,
+                   const void* v, int v_dtype, int64_t v_sb, int64_t v_ss, int64_t v_sh,
+                   int B, int S, int H, int D, int t_seq_len, const int32_t* sel, int topK,
+                   void* kn, void* vn, void* stream);
+
+/* Last error message of the calling thread ("" if none). */
+const char* icsa_last_error(void);
+
+/* Library version, major * 10000 + minor * 100 + patch. */
+int icsa_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ICSA_H_ */

@@ -1,0 +1,601 @@
+// C ABI of libicsa.so: argument validation, derived sizes, workspace layout and the launch
+// sequence of each entry point.  Declarations and contracts: include/icsa.h.
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "icsa_kernels.h"
+#include "../../include/icsa.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  return fail(ICSA_EHIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+#define ICSA_HIP_TRY(expr, what)                 \
+  do {                                           \
+    hipError_t e_ = (expr);                      \
+    if (e_ != hipSuccess) return hip_fail(e_, what); \
+  } while (0)
+
+int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
+int ceil_div(int a, int b) { return (a + b - 1) / b; }
+int elsize(int dtype) { return dtype == ICSA_F32 ? 4 : 2; }
+
+struct Sizes {
+  int NB, n_t, n_s, topK, Tkv, k_sparsity, n_peaked, n_diffuse, TKV_pad, NKV, top_k, NKVp;
+};
+
+// editing_sparse_attention.py:89-94, 126-129, 139, 164, 169-172, 189-198;
+// tilelang_host.py:151-152, 171.  Ratios are applied as int(n * ratio) in double precision,
+// which equals the reference's integer divisions for dyadic ratios.
+Sizes derive(int S, int t, double sparsity, double srr, double flat_ratio) {
+  Sizes z;
+  z.NB = ceil_div(S, ICSA_BLOCK);
+  z.n_t = t / ICSA_BLOCK;
+  z.n_s = z.NB - z.n_t;
+  z.topK = (int)((double)z.n_s * srr);
+  z.Tkv = t + z.topK * ICSA_BLOCK;
+  z.k_sparsity = std::max(1, (int)((double)z.n_t * sparsity));
+  z.n_peaked = (int)((double)z.NB * flat_ratio);
+  z.n_diffuse = z.NB - z.n_peaked;
+  z.TKV_pad = ceil_div(z.Tkv, ICSA_BLOCK) * ICSA_BLOCK;
+  z.NKV = z.TKV_pad / ICSA_BLOCK;
+  z.top_k = std::max(1, (int)(sparsity * (double)z.NKV));
+  z.NKVp = ceil_div(z.NKV, 64) * 64;
+  return z;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+bool row_ok(const void* p, int dtype, int64_t s0, int64_t s1, int64_t s2) {
+  const int64_t m = 16 / elsize(dtype);
+  return aligned16(p) && s0 % m == 0 && s1 % m == 0 && s2 % m == 0;
+}
+
+int check_dtype(int dt, const char* name) {
+  if (dt != ICSA_BF16 && dt != ICSA_F32) return fail(ICSA_EINVAL, "%s: dtype %d is not bf16 (0) or f32 (1)", name, dt);
+  return ICSA_OK;
+}
+
+struct Layout {
+  int64_t off[ICSA_WS_COUNT];
+  int64_t total;
+};
+
+Layout editing_layout(int B, int S, int H, const Sizes& z, int t, int q_dtype, int k_dtype) {
+  const int64_t BH = (int64_t)B * H;
+  const int64_t D = ICSA_D;
+  const int64_t Sp = (int64_t)z.NB * ICSA_BLOCK;
+  const bool unaligned = (t % ICSA_BLOCK) != 0;
+  int64_t sz[ICSA_WS_COUNT];
+  sz[ICSA_WS_QSUM] = BH * z.NB * D * 4;
+  sz[ICSA_WS_KSUM] = BH * z.NB * D * 4;
+  sz[ICSA_WS_VSUM] = BH * z.NB * D * 4;
+  sz[ICSA_WS_VT] = BH * D * Sp * 2;
+  sz[ICSA_WS_QB] = q_dtype == ICSA_F32 ? (int64_t)B * S * H * D * 2 : 0;
+  sz[ICSA_WS_KB] = k_dtype == ICSA_F32 ? (int64_t)B * S * H * D * 2 : 0;
+  sz[ICSA_WS_P] = BH * z.NB * z.NB * 4;
+  sz[ICSA_WS_OUTC] = BH * z.NB * D * 4;
+  sz[ICSA_WS_SHARP] = BH * z.NB * 4;
+  sz[ICSA_WS_SRCSCORE] = BH * std::max(z.n_s, 1) * 4;
+  sz[ICSA_WS_SEL] = BH * std::max(z.topK, 1) * 4;
+  sz[ICSA_WS_ORDER] = BH * z.NB * 4;
+  sz[ICSA_WS_KVMAP] = BH * z.NKV * 4;
+  sz[ICSA_WS_KC32] = BH * z.NKV * D * 4;
+  sz[ICSA_WS_KC] = BH * z.NKVp * D * 2;
+  sz[ICSA_WS_VCT] = BH * D * z.NKVp * 2;
+  sz[ICSA_WS_L3] = BH * std::max(z.n_diffuse, 1) * z.top_k * 4;
+  const int64_t Tp = z.TKV_pad;
+  sz[ICSA_WS_KN] = unaligned ? BH * Tp * D * 2 : 0;
+  sz[ICSA_WS_VN] = unaligned ? BH * Tp * D * 2 : 0;
+  sz[ICSA_WS_VTN] = unaligned ? BH * D * Tp * 2 : 0;
+  sz[ICSA_WS_NKSUM] = unaligned ? BH * z.NKV * D * 4 : 0;
+  sz[ICSA_WS_NVSUM] = unaligned ? BH * z.NKV * D * 4 : 0;
+  Layout L;
+  int64_t o = 0;
+  for (int i = 0; i < ICSA_WS_COUNT; ++i) {
+    L.off[i] = o;
+    o += align256(sz[i]);
+  }
+  L.total = o;
+  return L;
+}
+
+int validate_common(int B, int S, int H, int D) {
+  if (B <= 0 || S <= 0 || H <= 0) return fail(ICSA_EINVAL, "B, S, H must be positive (got %d, %d, %d)", B, S, H);
+  if (D != ICSA_D) return fail(ICSA_EUNSUPPORTED, "head dim D=%d unsupported (only 128)", D);
+  return ICSA_OK;
+}
+
+AlphaView make_alpha(const void* alpha, int alpha_dtype, int64_t a_sb, int64_t a_ss, int64_t a_sh,
+                     int64_t a_sd, float scalar) {
+  AlphaView a;
+  a.p = alpha;
+  a.sb = a_sb; a.ss = a_ss; a.sh = a_sh; a.sd = a_sd;
+  a.dtype = alpha_dtype;
+  a.scalar = scalar;
+  return a;
+}
+
+const float kLog2e = 1.4426950408889634f;
+
+}  // namespace
+
+extern "C" {
+
+const char* icsa_last_error(void) { return g_last_error.c_str(); }
+
+int icsa_version(void) { return 100; }
+
+int icsa_editing_sizes(int B, int S, int H, int D, int t_seq_len, double sparsity, double srr,
+                       double flat_ratio, int32_t* sizes_out) {
+  int rc = validate_common(B, S, H, D);
+  if (rc) return rc;
+  if (t_seq_len < 0 || t_seq_len > S) return fail(ICSA_EINVAL, "t_seq_len %d outside [0, S=%d]", t_seq_len, S);
+  if (!sizes_out) return fail(ICSA_EINVAL, "sizes_out is NULL");
+  Sizes z = derive(S, t_seq_len, sparsity, srr, flat_ratio);
+  const int v[12] = {z.NB, z.n_t, z.n_s, z.topK, z.Tkv, z.k_sparsity, z.n_peaked, z.n_diffuse,
+                     z.TKV_pad, z.NKV, z.top_k, z.NKVp};
+  std::memcpy(sizes_out, v, sizeof(v));
+  return ICSA_OK;
+}
+
+int64_t icsa_editing_workspace_layout(int B, int S, int H, int D, int t_seq_len, double sparsity,
+                                      double srr, double flat_ratio, int q_dtype, int k_dtype,
+                                      int64_t* offsets_out) {
+  if (validate_common(B, S, H, D)) return -1;
+  if (t_seq_len < 0 || t_seq_len > S) return -1;
+  Sizes z = derive(S, t_seq_len, sparsity, srr, flat_ratio);
+  Layout L = editing_layout(B, S, H, z, t_seq_len, q_dtype, k_dtype);
+  if (offsets_out) std::memcpy(offsets_out, L.off, sizeof(L.off));
+  return L.total;
+}
+
+int64_t icsa_editing_workspace_size(int B, int S, int H, int D, int t_seq_len, double sparsity,
+                                    double srr, double flat_ratio, int q_dtype, int k_dtype) {
+  return icsa_editing_workspace_layout(B, S, H, D, t_seq_len, sparsity, srr, flat_ratio, q_dtype,
+                                       k_dtype, nullptr);
+}
+
+int icsa_editing_sparse_attention(
+    const void* q, int q_dtype, int64_t q_sb, int64_t q_ss, int64_t q_sh,
+    const void* k, int k_dtype, int64_t k_sb, int64_t k_ss, int64_t k_sh,
+    const void* v, int v_dtype, int64_t v_sb, int64_t v_ss, int64_t v_sh,
+    int B, int S, int H, int D, int t_seq_len, double sparsity, double srr, double flat_ratio,
+    const void* alpha, int alpha_dtype, int64_t a_sb, int64_t a_ss, int64_t a_sh, int64_t a_sd,
+    float alpha_scalar,
+    void* out, int out_dtype, int64_t o_sb, int64_t o_ss, int64_t o_sh,
+    const int32_t* inject_sel, const int32_t* inject_order, const int32_t* inject_l3,
+    void* workspace, int64_t workspace_bytes, void* stream_) {
+  int rc = validate_common(B, S, H, D);
+  if (rc) return rc;
+  if ((rc = check_dtype(q_dtype, "q")) || (rc = check_dtype(k_dtype, "k")) ||
+      (rc = check_dtype(v_dtype, "v")) || (rc = check_dtype(out_dtype, "out")))
+    return rc;
+  if (alpha && (rc = check_dtype(alpha_dtype, "alpha"))) return rc;
+  if (!q || !k || !v || !out || !workspace) return fail(ICSA_EINVAL, "null q/k/v/out/workspace pointer");
+  if (!row_ok(q, q_dtype, q_sb, q_ss, q_sh) || !row_ok(k, k_dtype, k_sb, k_ss, k_sh) ||
+      !row_ok(v, v_dtype, v_sb, v_ss, v_sh) || !row_ok(out, out_dtype, o_sb, o_ss, o_sh))
+    return fail(ICSA_EINVAL, "q/k/v/out rows must be 16-byte aligned (pointer and strides)");
+  if (t_seq_len < 0 || t_seq_len > S) return fail(ICSA_EINVAL, "t_seq_len %d outside [0, S=%d]", t_seq_len, S);
+  if (!(sparsity > 0.0) || !(srr >= 0.0) || !(flat_ratio >= 0.0 && flat_ratio <= 1.0))
+    return fail(ICSA_EINVAL, "sparsity must be > 0, srr >= 0, flat_ratio in [0, 1]");
+  const Sizes z = derive(S, t_seq_len, sparsity, srr, flat_ratio);
+  if (z.Tkv <= 0) return fail(ICSA_EINVAL, "empty new KV (t_seq_len + 64 * topK == 0)");
+  if (z.n_t > 4096 || z.n_s > 4096 || z.NB > 4096)
+    return fail(ICSA_EUNSUPPORTED, "NB=%d blocks exceeds the 4096-block limit", z.NB);
+  if (z.NKV > 2048 || z.top_k > 512)
+    return fail(ICSA_EUNSUPPORTED, "NKV=%d / top_k=%d exceed limits (2048 / 512)", z.NKV, z.top_k);
+  const Layout L = editing_layout(B, S, H, z, t_seq_len, q_dtype, k_dtype);
+  if (workspace_bytes < L.total)
+    return fail(ICSA_EWORKSPACE, "workspace %lld bytes < required %lld", (long long)workspace_bytes,
+                (long long)L.total);
+  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+  char* ws = reinterpret_cast<char*>(workspace);
+  auto WS = [&](int slot) { return ws + L.off[slot]; };
+  const int BH = B * H;
+  const int64_t Sp = (int64_t)z.NB * ICSA_BLOCK;
+  const bool unaligned = (t_seq_len % ICSA_BLOCK) != 0;
+
+  // ---- stage 1: pooling (+ V transposed, + bf16 copies of f32 q/k) ----
+  PoolParams pp;
+  std::memset(&pp, 0, sizeof(pp));
+  pp.x[0] = TokTensor{q, q_sb, q_ss, q_sh, q_dtype};
+  pp.x[1] = TokTensor{k, k_sb, k_ss, k_sh, k_dtype};
+  pp.x[2] = TokTensor{v, v_sb, v_ss, v_sh, v_dtype};
+  pp.sums[0] = reinterpret_cast<float*>(WS(ICSA_WS_QSUM));
+  pp.sums[1] = reinterpret_cast<float*>(WS(ICSA_WS_KSUM));
+  pp.sums[2] = reinterpret_cast<float*>(WS(ICSA_WS_VSUM));
+  pp.xb[0] = q_dtype == ICSA_F32 ? reinterpret_cast<bf16*>(WS(ICSA_WS_QB)) : nullptr;
+  pp.xb[1] = k_dtype == ICSA_F32 ? reinterpret_cast<bf16*>(WS(ICSA_WS_KB)) : nullptr;
+  pp.xb_sb = (int64_t)S * H * ICSA_D; pp.xb_ss = (int64_t)H * ICSA_D; pp.xb_sh = ICSA_D;
+  pp.vt = reinterpret_cast<bf16*>(WS(ICSA_WS_VT));
+  pp.vt_sb = (int64_t)H * ICSA_D * Sp; pp.vt_sh = ICSA_D * Sp; pp.vt_sd = Sp;
+  pp.vt_src = 2;
+  pp.B = B; pp.S = S; pp.H = H; pp.NB = z.NB;
+  ICSA_HIP_TRY(launch_pool(pp, stream), "pool");
+
+  // bf16 views of q / k used by the attention kernels
+  const bf16* qb = q_dtype == ICSA_BF16 ? reinterpret_cast<const bf16*>(q) : pp.xb[0];
+  const int64_t qb_sb = q_dtype == ICSA_BF16 ? q_sb : pp.xb_sb;
+  const int64_t qb_ss = q_dtype == ICSA_BF16 ? q_ss : pp.xb_ss;
+  const int64_t qb_sh = q_dtype == ICSA_BF16 ? q_sh : pp.xb_sh;
+  const bf16* kb = k_dtype == ICSA_BF16 ? reinterpret_cast<const bf16*>(k) : pp.xb[1];
+  const int64_t kb_sb = k_dtype == ICSA_BF16 ? k_sb : pp.xb_sb;
+  const int64_t kb_ss = k_dtype == ICSA_BF16 ? k_ss : pp.xb_ss;
+  const int64_t kb_sh = k_dtype == ICSA_BF16 ? k_sh : pp.xb_sh;
+
+  // ---- stage 2: compressed attention, retrieval, split ----
+  CompressedParams cp;
+  cp.qsum = pp.sums[0]; cp.ksum = pp.sums[1]; cp.vsum = pp.sums[2];
+  cp.P = reinterpret_cast<float*>(WS(ICSA_WS_P));
+  cp.out_c = reinterpret_cast<float*>(WS(ICSA_WS_OUTC));
+  cp.sharp = reinterpret_cast<float*>(WS(ICSA_WS_SHARP));
+  cp.BH = BH; cp.NB = z.NB; cp.S = S; cp.n_t = z.n_t; cp.k_sparsity = z.k_sparsity;
+  ICSA_HIP_TRY(launch_compressed(cp, stream), "compressed attention");
+
+  int32_t* sel = reinterpret_cast<int32_t*>(WS(ICSA_WS_SEL));
+  int32_t* order = reinterpret_cast<int32_t*>(WS(ICSA_WS_ORDER));
+  if (inject_sel && z.topK > 0)
+    ICSA_HIP_TRY(hipMemcpyAsync(sel, inject_sel, (size_t)BH * z.topK * 4, hipMemcpyDeviceToDevice, stream),
+                 "inject sel");
+  if (inject_order)
+    ICSA_HIP_TRY(hipMemcpyAsync(order, inject_order, (size_t)BH * z.NB * 4, hipMemcpyDeviceToDevice, stream),
+                 "inject order");
+  SelectParams sp;
+  sp.P = cp.P; sp.sharp = cp.sharp;
+  sp.src_score = reinterpret_cast<float*>(WS(ICSA_WS_SRCSCORE));
+  sp.sel = sel; sp.order = order;
+  sp.kvmap = reinterpret_cast<int*>(WS(ICSA_WS_KVMAP));
+  sp.BH = BH; sp.NB = z.NB; sp.n_t = z.n_t; sp.n_s = z.n_s; sp.topK = z.topK; sp.NKV = z.NKV;
+  sp.materialized = unaligned ? 1 : 0;
+  sp.inject_sel = inject_sel ? 1 : 0;
+  sp.inject_order = inject_order ? 1 : 0;
+  ICSA_HIP_TRY(launch_select(sp, stream), "select");
+
+  // ---- new-KV block sums (in place for aligned t, materialised otherwise) ----
+  NewKvSumsParams np;
+  np.kc32 = reinterpret_cast<float*>(WS(ICSA_WS_KC32));
+  np.kc = reinterpret_cast<bf16*>(WS(ICSA_WS_KC));
+  np.vct = reinterpret_cast<bf16*>(WS(ICSA_WS_VCT));
+  np.BH = BH; np.NKV = z.NKV; np.NKVp = z.NKVp;
+  const bf16* sk_k;            // key source of the sparse kernel
+  int64_t sk_sb, sk_st, sk_sh;
+  const bf16* sk_vt;
+  int64_t sk_vsb, sk_vsh, sk_vsd;
+  int sk_Sk;
+  if (!unaligned) {
+    np.ksum = pp.sums[1]; np.vsum = pp.sums[2];
+    np.kvmap = sp.kvmap; np.map_identity = 0; np.Nsrc = z.NB;
+    sk_k = kb; sk_sb = kb_sb; sk_st = kb_ss; sk_sh = kb_sh;
+    sk_vt = pp.vt; sk_vsb = pp.vt_sb; sk_vsh = pp.vt_sh; sk_vsd = pp.vt_sd;
+    sk_Sk = S;
+  } else {
+    const int64_t Tp = z.TKV_pad;
+    GatherParams gp;
+    gp.k = TokTensor{k, k_sb, k_ss, k_sh, k_dtype};
+    gp.v = TokTensor{v, v_sb, v_ss, v_sh, v_dtype};
+    gp.sel = sel;
+    gp.kn = reinterpret_cast<bf16*>(WS(ICSA_WS_KN));
+    gp.vn = reinterpret_cast<bf16*>(WS(ICSA_WS_VN));
+    gp.B = B; gp.H = H; gp.S = S; gp.t = t_seq_len; gp.topK = z.topK; gp.Tkv = z.Tkv; gp.Tp = (int)Tp;
+    ICSA_HIP_TRY(launch_gather(gp, stream), "gather new KV");
+    PoolParams pn;
+    std::memset(&pn, 0, sizeof(pn));
+    // materialised [B*H, Tp, D] viewed as [B, Tp, H, D]-strided tensors
+    pn.x[1] = TokTensor{gp.kn, (int64_t)H * Tp * ICSA_D, ICSA_D, Tp * ICSA_D, ICSA_BF16};
+    pn.x[2] = TokTensor{gp.vn, (int64_t)H * Tp * ICSA_D, ICSA_D, Tp * ICSA_D, ICSA_BF16};
+    pn.sums[1] = reinterpret_cast<float*>(WS(ICSA_WS_NKSUM));
+    pn.sums[2] = reinterpret_cast<float*>(WS(ICSA_WS_NVSUM));
+    pn.vt = reinterpret_cast<bf16*>(WS(ICSA_WS_VTN));
+    pn.vt_sb = (int64_t)H * ICSA_D * Tp; pn.vt_sh = ICSA_D * Tp; pn.vt_sd = Tp;
+    pn.vt_src = 2;
+    pn.B = B; pn.S = (int)Tp; pn.H = H; pn.NB = z.NKV;
+    ICSA_HIP_TRY(launch_pool(pn, stream), "pool new KV");
+    np.ksum = pn.sums[1]; np.vsum = pn.sums[2];
+    np.kvmap = nullptr; np.map_identity = 1; np.Nsrc = z.NKV;
+    sk_k = gp.kn; sk_sb = (int64_t)H * Tp * ICSA_D; sk_st = ICSA_D; sk_sh = Tp * ICSA_D;
+    sk_vt = pn.vt; sk_vsb = pn.vt_sb; sk_vsh = pn.vt_sh; sk_vsd = pn.vt_sd;
+    sk_Sk = (int)Tp;
+  }
+  if (z.n_diffuse > 0) ICSA_HIP_TRY(launch_newkv_sums(np, stream), "new-KV sums");
+
+  // ---- level-3 selection for the diffuse blocks ----
+  int32_t* l3 = reinterpret_cast<int32_t*>(WS(ICSA_WS_L3));
+  if (z.n_diffuse > 0) {
+    if (inject_l3) {
+      ICSA_HIP_TRY(hipMemcpyAsync(l3, inject_l3, (size_t)BH * z.n_diffuse * z.top_k * 4,
+                                  hipMemcpyDeviceToDevice, stream), "inject l3");
+    } else {
+      Level3Params lp;
+      lp.qsum = pp.sums[0]; lp.rows = order; lp.rows_offset = z.n_peaked; lp.rows_stride = z.NB;
+      lp.kc32 = np.kc32; lp.idx = l3;
+      lp.BH = BH; lp.NQsrc = z.NB; lp.n_rows = z.n_diffuse; lp.NKV = z.NKV; lp.top_k = z.top_k;
+      ICSA_HIP_TRY(launch_level3(lp, stream), "level-3 top-k");
+    }
+  }
+
+  const AlphaView av = make_alpha(alpha, alpha_dtype, a_sb, a_ss, a_sh, a_sd, alpha_scalar);
+  OutView ov{out, o_sb, o_ss, o_sh, out_dtype};
+  const float scale_log2 = kLog2e / std::sqrt((float)ICSA_D);
+
+  // ---- stage 4: sparse piecewise attention on the diffuse blocks ----
+  if (z.n_diffuse > 0) {
+    SparseParams s;
+    s.q = qb; s.q_sb = qb_sb; s.q_ss = qb_ss; s.q_sh = qb_sh;
+    s.k = sk_k; s.k_sb = sk_sb; s.k_st = sk_st; s.k_sh = sk_sh;
+    s.vt = sk_vt; s.vt_sb = sk_vsb; s.vt_sh = sk_vsh; s.vt_sd = sk_vsd;
+    s.B = B; s.H = H; s.Sq = S; s.Sk = sk_Sk;
+    s.qblocks = order; s.qb_offset = z.n_peaked; s.qb_stride = z.NB; s.n_qblk = z.n_diffuse;
+    s.kvmap = sp.kvmap; s.kvmap_identity = unaligned ? 1 : 0;
+    s.idx = l3; s.top_k = z.top_k; s.NKV = z.NKV; s.NKVp = z.NKVp;
+    s.kc = np.kc; s.vct = np.vct;
+    s.out_c = cp.out_c; s.nb_q = z.NB;
+    s.alpha = av; s.out = ov; s.scale_log2 = scale_log2;
+    ICSA_HIP_TRY(launch_sparse(s, stream), "sparse attention");
+  }
+
+  // ---- stage 3: flash attention on the peaked blocks ----
+  if (z.n_peaked > 0) {
+    FlashParams f;
+    f.q = qb; f.q_sb = qb_sb; f.q_ss = qb_ss; f.q_sh = qb_sh;
+    f.k = kb; f.k_sb = kb_sb; f.k_ss = kb_ss; f.k_sh = kb_sh;
+    f.vt = pp.vt; f.vt_sb = pp.vt_sb; f.vt_sh = pp.vt_sh; f.vt_sd = pp.vt_sd;
+    f.B = B; f.H = H; f.Sq = S; f.Sk = S;
+    f.qblocks = order; f.qb_offset = 0; f.qb_stride = z.NB; f.n_qblk = z.n_peaked;
+    f.t_limit = t_seq_len; f.n_tgt_tiles = ceil_div(t_seq_len, ICSA_BLOCK);
+    f.sel = sel; f.sel_stride = std::max(z.topK, 1); f.n_sel = z.topK; f.sel_base = z.n_t;
+    f.out_c = cp.out_c; f.nb_q = z.NB;
+    f.alpha = av; f.out = ov; f.scale_log2 = scale_log2;
+    ICSA_HIP_TRY(launch_flash(f, stream), "flash attention");
+  }
+  return ICSA_OK;
+}
+
+// ---------------------------------------------------------------------------------------
+
+namespace {
+struct SpLayout {
+  int64_t qsum, ksum, vsum, vt, kc32, kc, vct, idx, total;
+};
+SpLayout sparse_layout(int B, int H, int TQ, int TKV, double sparsity) {
+  const int64_t BH = (int64_t)B * H;
+  const int NQ = TQ / ICSA_BLOCK, NKV = TKV / ICSA_BLOCK;
+  const int NKVp = ceil_div(NKV, 64) * 64;
+  const int top_k = std::max(1, (int)(sparsity * (double)NKV));
+  SpLayout L;
+  int64_t o = 0;
+  L.qsum = o; o += align256(BH * NQ * ICSA_D * 4);
+  L.ksum = o; o += align256(BH * NKV * ICSA_D * 4);
+  L.vsum = o; o += align256(BH * NKV * ICSA_D * 4);
+  L.vt = o; o += align256(BH * ICSA_D * (int64_t)TKV * 2);
+  L.kc32 = o; o += align256(BH * NKV * ICSA_D * 4);
+  L.kc = o; o += align256(BH * NKVp * ICSA_D * 2);
+  L.vct = o; o += align256(BH * ICSA_D * NKVp * 2);
+  L.idx = o; o += align256(BH * NQ * top_k * 4);
+  L.total = o;
+  return L;
+}
+}  // namespace
+
+int64_t icsa_sparse_piecewise_workspace_size(int B, int H, int TQ, int TKV, int D, double sparsity) {
+  if (B <= 0 || H <= 0 || TQ <= 0 || TKV <= 0 || D != ICSA_D) return -1;
+  return sparse_layout(B, H, TQ, TKV, sparsity).total;
+}
+
+int icsa_sparse_piecewise_attn(
+    const void* q, int64_t q_sb, int64_t q_sh, int64_t q_st,
+    const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st,
+    const void* v, int64_t v_sb, int64_t v_sh, int64_t v_st,
+    int B, int H, int TQ, int TKV, int D, double sparsity,
+    const int32_t* inject_idx, int32_t* idx_out,
+    void* out, int64_t o_sb, int64_t o_sh, int64_t o_st,
+    void* workspace, int64_t workspace_bytes, void* stream_) {
+  int rc = validate_common(B, TQ, H, D);
+  if (rc) return rc;
+  if (TKV <= 0) return fail(ICSA_EINVAL, "TKV must be positive");
+  if (TQ % ICSA_BLOCK || TKV % ICSA_BLOCK)
+    return fail(ICSA_EINVAL, "TQ/TKV must be divisible by the block size 64 (got %d, %d)", TQ, TKV);
+  if (!q || !k || !v || !out || !workspace) return fail(ICSA_EINVAL, "null q/k/v/out/workspace pointer");
+  if (!row_ok(q, ICSA_BF16, q_sb, q_sh, q_st) || !row_ok(k, ICSA_BF16, k_sb, k_sh, k_st) ||
+      !row_ok(v, ICSA_BF16, v_sb, v_sh, v_st) || !row_ok(out, ICSA_BF16, o_sb, o_sh, o_st))
+    return fail(ICSA_EINVAL, "q/k/v/out rows must be 16-byte aligned (pointer and strides)");
+  if (!(sparsity > 0.0)) return fail(ICSA_EINVAL, "sparsity must be > 0");
+  const int NQ = TQ / ICSA_BLOCK, NKV = TKV / ICSA_BLOCK;
+  const int NKVp = ceil_div(NKV, 64) * 64;
+  const int top_k = std::max(1, (int)(sparsity * (double)NKV));
+  if (NKV > 2048 || top_k > 512 || top_k > NKV)
+    return fail(ICSA_EUNSUPPORTED, "NKV=%d / top_k=%d exceed limits (2048 / 512)", NKV, top_k);
+  const SpLayout L = sparse_layout(B, H, TQ, TKV, sparsity);
+  if (workspace_bytes < L.total)
+    return fail(ICSA_EWORKSPACE, "workspace %lld bytes < required %lld", (long long)workspace_bytes,
+                (long long)L.total);
+  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+  char* ws = reinterpret_cast<char*>(workspace);
+  const int BH = B * H;
+
+  PoolParams pq;
+  std::memset(&pq, 0, sizeof(pq));
+  pq.x[0] = TokTensor{q, q_sb, q_st, q_sh, ICSA_BF16};
+  pq.sums[0] = reinterpret_cast<float*>(ws + L.qsum);
+  pq.B = B; pq.S = TQ; pq.H = H; pq.NB = NQ;
+  ICSA_HIP_TRY(launch_pool(pq, stream), "pool q");
+  PoolParams pk;
+  std::memset(&pk, 0, sizeof(pk));
+  pk.x[1] = TokTensor{k, k_sb, k_st, k_sh, ICSA_BF16};
+  pk.x[2] = TokTensor{v, v_sb, v_st, v_sh, ICSA_BF16};
+  pk.sums[1] = reinterpret_cast<float*>(ws + L.ksum);
+  pk.sums[2] = reinterpret_cast<float*>(ws + L.vsum);
+  pk.vt = reinterpret_cast<bf16*>(ws + L.vt);
+  pk.vt_sb = (int64_t)H * ICSA_D * TKV; pk.vt_sh = (int64_t)ICSA_D * TKV; pk.vt_sd = TKV;
+  pk.vt_src = 2;
+  pk.B = B; pk.S = TKV; pk.H = H; pk.NB = NKV;
+  ICSA_HIP_TRY(launch_pool(pk, stream), "pool k/v");
+
+  NewKvSumsParams np;
+  np.ksum = pk.sums[1]; np.vsum = pk.sums[2]; np.kvmap = nullptr; np.map_identity = 1;
+  np.kc32 = reinterpret_cast<float*>(ws + L.kc32);
+  np.kc = reinterpret_cast<bf16*>(ws + L.kc);
+  np.vct = reinterpret_cast<bf16*>(ws + L.vct);
+  np.BH = BH; np.Nsrc = NKV; np.NKV = NKV; np.NKVp = NKVp;
+  ICSA_HIP_TRY(launch_newkv_sums(np, stream), "block sums");
+
+  int32_t* idx = reinterpret_cast<int32_t*>(ws + L.idx);
+  if (inject_idx) {
+    ICSA_HIP_TRY(hipMemcpyAsync(idx, inject_idx, (size_t)BH * NQ * top_k * 4, hipMemcpyDeviceToDevice,
+                                stream), "inject idx");
+  } else {
+    Level3Params lp;
+    lp.qsum = pq.sums[0]; lp.rows = nullptr; lp.rows_offset = 0; lp.rows_stride = 0;
+    lp.kc32 = np.kc32; lp.idx = idx;
+    lp.BH = BH; lp.NQsrc = NQ; lp.n_rows = NQ; lp.NKV = NKV; lp.top_k = top_k;
+    ICSA_HIP_TRY(launch_level3(lp, stream), "block top-k");
+  }
+  if (idx_out)
+    ICSA_HIP_TRY(hipMemcpyAsync(idx_out, idx, (size_t)BH * NQ * top_k * 4, hipMemcpyDeviceToDevice, stream),
+                 "copy idx");
+
+  SparseParams s;
+  s.q = reinterpret_cast<const bf16*>(q); s.q_sb = q_sb; s.q_ss = q_st; s.q_sh = q_sh;
+  s.k = reinterpret_cast<const bf16*>(k); s.k_sb = k_sb; s.k_st = k_st; s.k_sh = k_sh;
+  s.vt = pk.vt; s.vt_sb = pk.vt_sb; s.vt_sh = pk.vt_sh; s.vt_sd = pk.vt_sd;
+  s.B = B; s.H = H; s.Sq = TQ; s.Sk = TKV;
+  s.qblocks = nullptr; s.qb_offset = 0; s.qb_stride = 0; s.n_qblk = NQ;
+  s.kvmap = nullptr; s.kvmap_identity = 1;
+  s.idx = idx; s.top_k = top_k; s.NKV = NKV; s.NKVp = NKVp;
+  s.kc = np.kc; s.vct = np.vct;
+  s.out_c = nullptr; s.nb_q = NQ;
+  s.alpha = make_alpha(nullptr, ICSA_F32, 0, 0, 0, 0, 0.f);
+  s.out = OutView{out, o_sb, o_st, o_sh, ICSA_BF16};
+  s.scale_log2 = kLog2e / std::sqrt((float)ICSA_D);
+  ICSA_HIP_TRY(launch_sparse(s, stream), "sparse attention");
+  return ICSA_OK;
+}
+
+// ---------------------------------------------------------------------------------------
+
+int64_t icsa_flash_attn_workspace_size(int B, int Sk, int H, int D) {
+  if (B <= 0 || Sk <= 0 || H <= 0 || D != ICSA_D) return -1;
+  return align256((int64_t)B * H * ICSA_D * ceil_div(Sk, ICSA_BLOCK) * ICSA_BLOCK * 2);
+}
+
+int icsa_flash_attn(const void* q, int64_t q_sb, int64_t q_ss, int64_t q_sh,
+                    const void* k, int64_t k_sb, int64_t k_ss, int64_t k_sh,
+                    const void* v, int64_t v_sb, int64_t v_ss, int64_t v_sh,
+                    int B, int Sq, int Sk, int H, int D,
+                    void* out, int out_dtype, int64_t o_sb, int64_t o_ss, int64_t o_sh,
+                    void* workspace, int64_t workspace_bytes, void* stream_) {
+  int rc = validate_common(B, Sq, H, D);
+  if (rc) return rc;
+  if (Sk <= 0) return fail(ICSA_EINVAL, "Sk must be positive");
+  if ((rc = check_dtype(out_dtype, "out"))) return rc;
+  if (!q || !k || !v || !out || !workspace) return fail(ICSA_EINVAL, "null q/k/v/out/workspace pointer");
+  if (!row_ok(q, ICSA_BF16, q_sb, q_ss, q_sh) || !row_ok(k, ICSA_BF16, k_sb, k_ss, k_sh) ||
+      !row_ok(v, ICSA_BF16, v_sb, v_ss, v_sh) || !row_ok(out, out_dtype, o_sb, o_ss, o_sh))
+    return fail(ICSA_EINVAL, "q/k/v/out rows must be 16-byte aligned (pointer and strides)");
+  const int64_t need = icsa_flash_attn_workspace_size(B, Sk, H, D);
+  if (workspace_bytes < need)
+    return fail(ICSA_EWORKSPACE, "workspace %lld bytes < required %lld", (long long)workspace_bytes,
+                (long long)need);
+  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+  const int NBk = ceil_div(Sk, ICSA_BLOCK);
+  const int64_t Skp = (int64_t)NBk * ICSA_BLOCK;
+  PoolParams pv;
+  std::memset(&pv, 0, sizeof(pv));
+  pv.x[2] = TokTensor{v, v_sb, v_ss, v_sh, ICSA_BF16};
+  pv.vt = reinterpret_cast<bf16*>(workspace);
+  pv.vt_sb = (int64_t)H * ICSA_D * Skp; pv.vt_sh = ICSA_D * Skp; pv.vt_sd = Skp;
+  pv.vt_src = 2;
+  pv.B = B; pv.S = Sk; pv.H = H; pv.NB = NBk;
+  ICSA_HIP_TRY(launch_pool(pv, stream), "transpose v");
+  FlashParams f;
+  f.q = reinterpret_cast<const bf16*>(q); f.q_sb = q_sb; f.q_ss = q_ss; f.q_sh = q_sh;
+  f.k = reinterpret_cast<const bf16*>(k); f.k_sb = k_sb; f.k_ss = k_ss; f.k_sh = k_sh;
+  f.vt = pv.vt; f.vt_sb = pv.vt_sb; f.vt_sh = pv.vt_sh; f.vt_sd = pv.vt_sd;
+  f.B = B; f.H = H; f.Sq = Sq; f.Sk = Sk;
+  f.qblocks = nullptr; f.qb_offset = 0; f.qb_stride = 0; f.n_qblk = ceil_div(Sq, ICSA_BLOCK);
+  f.t_limit = Sk; f.n_tgt_tiles = NBk;
+  f.sel = nullptr; f.sel_stride = 0; f.n_sel = 0; f.sel_base = 0;
+  f.out_c = nullptr; f.nb_q = 0;
+  f.alpha = make_alpha(nullptr, ICSA_F32, 0, 0, 0, 0, 0.f);
+  f.out = OutView{out, o_sb, o_ss, o_sh, out_dtype};
+  f.scale_log2 = kLog2e / std::sqrt((float)ICSA_D);
+  ICSA_HIP_TRY(launch_flash(f, stream), "flash attention");
+  return ICSA_OK;
+}
+
+int icsa_pool(const void* q, int q_dtype, int64_t q_sb, int64_t q_ss, int64_t q_sh,
+              const void* k, int k_dtype, int64_t k_sb, int64_t k_ss, int64_t k_sh,
+              const void* v, int v_dtype, int64_t v_sb, int64_t v_ss, int64_t v_sh,
+              int B, int S, int H, int D, float* qsum, float* ksum, float* vsum, void* vt,
+              void* stream_) {
+  int rc = validate_common(B, S, H, D);
+  if (rc) return rc;
+  PoolParams pp;
+  std::memset(&pp, 0, sizeof(pp));
+  const void* src[3] = {q, k, v};
+  const int dt[3] = {q_dtype, k_dtype, v_dtype};
+  const int64_t st[3][3] = {{q_sb, q_ss, q_sh}, {k_sb, k_ss, k_sh}, {v_sb, v_ss, v_sh}};
+  float* sums[3] = {qsum, ksum, vsum};
+  for (int i = 0; i < 3; ++i) {
+    if (!src[i]) continue;
+    if ((rc = check_dtype(dt[i], "input"))) return rc;
+    if (!row_ok(src[i], dt[i], st[i][0], st[i][1], st[i][2]))
+      return fail(ICSA_EINVAL, "input %d rows must be 16-byte aligned", i);
+    pp.x[i] = TokTensor{src[i], st[i][0], st[i][1], st[i][2], dt[i]};
+    pp.sums[i] = sums[i];
+  }
+  if (vt && !v) return fail(ICSA_EINVAL, "vt requested without v");
+  const int NB = ceil_div(S, ICSA_BLOCK);
+  const int64_t Sp = (int64_t)NB * ICSA_BLOCK;
+  pp.vt = reinterpret_cast<bf16*>(vt);
+  pp.vt_sb = (int64_t)H * ICSA_D * Sp; pp.vt_sh = ICSA_D * Sp; pp.vt_sd = Sp;
+  pp.vt_src = 2;
+  pp.B = B; pp.S = S; pp.H = H; pp.NB = NB;
+  ICSA_HIP_TRY(launch_pool(pp, reinterpret_cast<hipStream_t>(stream_)), "pool");
+  return ICSA_OK;
+}
+
+int icsa_gather_kv(const void* k, int k_dtype, int64_t k_sb, int64_t k_ss, int64_t k_sh,
+                   const void* v, int v_dtype, int64_t v_sb, int64_t v_ss, int64_t v_sh,
+                   int B, int S, int H, int D, int t_seq_len, const int32_t* sel, int topK,
+                   void* kn, void* vn, void* stream_) {
+  int rc = validate_common(B, S, H, D);
+  if (rc) return rc;
+  if ((rc = check_dtype(k_dtype, "k")) || (rc = check_dtype(v_dtype, "v"))) return rc;
+  if (!k || !v || !kn || !vn || (topK > 0 && !sel)) return fail(ICSA_EINVAL, "null pointer");
+  if (t_seq_len < 0 || t_seq_len > S || topK < 0) return fail(ICSA_EINVAL, "bad t_seq_len / topK");
+  if (!row_ok(k, k_dtype, k_sb, k_ss, k_sh) || !row_ok(v, v_dtype, v_sb, v_ss, v_sh))
+    return fail(ICSA_EINVAL, "k/v rows must be 16-byte aligned");
+  GatherParams gp;
+  gp.k = TokTensor{k, k_sb, k_ss, k_sh, k_dtype};
+  gp.v = TokTensor{v, v_sb, v_ss, v_sh, v_dtype};
+  gp.sel = sel;
+  gp.kn = reinterpret_cast<bf16*>(kn);
+  gp.vn = reinterpret_cast<bf16*>(vn);
+  gp.B = B; gp.H = H; gp.S = S; gp.t = t_seq_len; gp.topK = topK;
+  gp.Tkv = t_seq_len + topK * ICSA_BLOCK;
+  gp.Tp = ceil_div(gp.Tkv, ICSA_BLOCK) * ICSA_BLOCK;
+  if (gp.Tp == 0) return ICSA_OK;
+  ICSA_HIP_TRY(launch_gather(gp, reinterpret_cast<hipStream_t>(stream_)), "gather");
+  return ICSA_OK;
+}
+
+}  // extern "C"

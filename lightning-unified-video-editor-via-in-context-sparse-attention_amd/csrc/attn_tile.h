@@ -1,0 +1,207 @@
+// Tile toolkit shared by the flash-attention (stage 3) and sparse piecewise (stage 4)
+// kernels.  One wave owns 32 queries; a key tile is 64 keys x 128 dims.
+//
+// Orientation: the score tile is computed transposed, S^T[key][query] = K Q^T, with
+// v_mfma_f32_32x32x16_bf16 (A = K rows from LDS, B = Q^T held in registers).  The result
+// layout puts one query per lane (lane % 32) and 16 of the 32 keys of a sub-tile in each
+// lane; the other 16 keys of that query sit in lane ^ 32.  Row max / row sum therefore
+// need one v_permlane32_swap per tile instead of a 32-lane reduction.
+//
+// PV: O^T[d][query] += V^T[d][key] P^T[key][query] with A = V^T from LDS and B = P^T
+// straight from the score registers.  The keys one lane holds for a 16-key MFMA step are
+// {0-3, 8-11} (lanes 0-31) and {4-7, 12-15} (lanes 32-63); V^T is stored with bits 2 and
+// 3 of the token index swapped (kv_slot) so those 8 keys are one contiguous 16-byte read.
+//
+// LDS tiles are XOR-swizzled in 16-byte chunks so the MFMA operand reads are free of bank
+// conflicts: K tile row r chunk c at c ^ (r & 15); V^T tile row d chunk c at c ^ ((d>>1)&7).
+#pragma once
+
+#include "icsa_common.h"
+
+#define ATT_BN 64                         // keys per tile
+#define K_TILE_BYTES (ATT_BN * ICSA_D * 2)    // 16 KB
+#define V_TILE_BYTES (ICSA_D * ATT_BN * 2)    // 16 KB
+
+// Register staging of one K + V^T tile for a workgroup of NT threads (NT = 256 or 128).
+template <int NT>
+struct TileRegs {
+  static constexpr int N = (ATT_BN * ICSA_D / 8) / NT;   // 16-byte chunks per thread per tile
+  u32x4 k[N];
+  u32x4 v[N];
+};
+
+__device__ __forceinline__ int k_lds_off(int row, int chunk) {     // in bf16 elements
+  return row * ICSA_D + ((chunk ^ (row & 15)) << 3);
+}
+__device__ __forceinline__ int v_lds_off(int d, int chunk) {
+  return d * ATT_BN + ((chunk ^ ((d >> 1) & 7)) << 3);
+}
+
+// Global -> registers for one tile.  krow0: pointer to key row 0 of the tile, k_rs: key row
+// stride (elements), k_valid: rows < k_valid are real (others read as 0).  vcol0: pointer
+// to V^T row d = 0 at the tile's first slot, v_rs: V^T row stride; v_zero: zero V^T tile.
+template <int NT>
+__device__ __forceinline__ void tile_load_regs(TileRegs<NT>& r, const bf16* krow0, int64_t k_rs,
+                                               int k_valid, const bf16* vcol0, int64_t v_rs,
+                                               bool v_zero) {
+  constexpr int N = TileRegs<NT>::N;
+  constexpr int KR = NT / 16;          // key rows covered per pass
+  constexpr int VR = NT / 8;           // V^T rows covered per pass
+  const int t = threadIdx.x;
+  const int kr = t >> 4, kc = t & 15;
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const int row = kr + KR * i;
+    if (row < k_valid)
+      r.k[i] = *reinterpret_cast<const u32x4*>(krow0 + (int64_t)row * k_rs + 8 * kc);
+    else
+      r.k[i] = u32x4{0u, 0u, 0u, 0u};
+  }
+  const int vd = t >> 3, vc = t & 7;
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const int d = vd + VR * i;
+    if (!v_zero)
+      r.v[i] = *reinterpret_cast<const u32x4*>(vcol0 + (int64_t)d * v_rs + 8 * vc);
+    else
+      r.v[i] = u32x4{0u, 0u, 0u, 0u};
+  }
+}
+
+template <int NT>
+__device__ __forceinline__ void tile_store_lds(const TileRegs<NT>& r, bf16* ks, bf16* vs) {
+  constexpr int N = TileRegs<NT>::N;
+  constexpr int KR = NT / 16;
+  constexpr int VR = NT / 8;
+  const int t = threadIdx.x;
+  const int kr = t >> 4, kc = t & 15;
+#pragma unroll
+  for (int i = 0; i < N; ++i)
+    *reinterpret_cast<u32x4*>(ks + k_lds_off(kr + KR * i, kc)) = r.k[i];
+  const int vd = t >> 3, vc = t & 7;
+#pragma unroll
+  for (int i = 0; i < N; ++i)
+    *reinterpret_cast<u32x4*>(vs + v_lds_off(vd + VR * i, vc)) = r.v[i];
+}
+
+// Q^T operand of one wave: 32 queries (rows qrow0 + lane%32, rows >= q_valid are zero).
+__device__ __forceinline__ void load_q_frags(bf16x8 qf[8], const bf16* qrow0, int64_t q_rs,
+                                             int q_valid) {
+  const int lane = threadIdx.x & 63;
+  const int li = lane & 31, hl = lane >> 5;
+  if (li < q_valid) {
+    const bf16* src = qrow0 + (int64_t)li * q_rs + 8 * hl;
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) qf[kk] = *reinterpret_cast<const bf16x8*>(src + 16 * kk);
+  } else {
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) {
+      bf16x8 z;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) z[e] = (bf16)0.f;
+      qf[kk] = z;
+    }
+  }
+}
+
+// S^T for the 64 keys of an LDS K tile: s[ks] covers keys 32*ks .. 32*ks + 31.
+__device__ __forceinline__ void qk_tile(floatx16 s[2], const bf16* ks, const bf16x8 qf[8]) {
+  const int lane = threadIdx.x & 63;
+  const int li = lane & 31, hl = lane >> 5;
+#pragma unroll
+  for (int sub = 0; sub < 2; ++sub) {
+    floatx16 acc = {};
+    const int row = 32 * sub + li;
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) {
+      const bf16x8 a = *reinterpret_cast<const bf16x8*>(ks + k_lds_off(row, 2 * kk + hl));
+      acc = mfma32x32x16(a, qf[kk], acc);
+    }
+    s[sub] = acc;
+  }
+}
+
+// O^T[4 d-subtiles] += V^T P^T for one tile; p[m] holds the bf16 probabilities of 16-key
+// step m (m = 0..3).
+__device__ __forceinline__ void pv_tile(floatx16 o[4], const bf16* vs, const bf16x8 p[4]) {
+  const int lane = threadIdx.x & 63;
+  const int li = lane & 31, hl = lane >> 5;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+#pragma unroll
+    for (int ds = 0; ds < 4; ++ds) {
+      const bf16x8 a = *reinterpret_cast<const bf16x8*>(vs + v_lds_off(32 * ds + li, 2 * m + hl));
+      o[ds] = mfma32x32x16(a, p[m], o[ds]);
+    }
+  }
+}
+
+// bf16 B operand of PV step m from the score registers (keys of sub-tile m/2, half m%2).
+__device__ __forceinline__ void pack_p(bf16x8 p[4], const floatx16 s[2]) {
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) p[m][e] = (bf16)s[m >> 1][8 * (m & 1) + e];
+  }
+}
+
+// Residual epilogue: out[tok, d] = o[query][d] * inv_l + alpha(b,tok,h,d) * out_c[blk][d].
+// o_lds: this wave's [32][O_LDS_STRIDE] fp32 staging area.  Rows >= rows_valid skipped.
+#define O_LDS_STRIDE (ICSA_D + 1)
+
+__device__ __forceinline__ void stage_o(float* o_lds, const floatx16 o[4], float inv_l) {
+  const int lane = threadIdx.x & 63;
+  const int li = lane & 31;
+#pragma unroll
+  for (int ds = 0; ds < 4; ++ds) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) o_lds[li * O_LDS_STRIDE + 32 * ds + acc_row(i, lane)] = o[ds][i] * inv_l;
+  }
+}
+
+__device__ __forceinline__ float alpha_at(const AlphaView& a, int b, int tok, int h, int d) {
+  if (a.p == nullptr) return a.scalar;
+  const int64_t off = (int64_t)b * a.sb + (int64_t)tok * a.ss + (int64_t)h * a.sh + (int64_t)d * a.sd;
+  if (a.dtype == ICSA_DT_F32) return reinterpret_cast<const float*>(a.p)[off];
+  return (float)reinterpret_cast<const bf16*>(a.p)[off];
+}
+
+// Stores the wave's 32 staged rows starting at token tok0 (rows tok0 + r for r < rows_valid).
+__device__ __forceinline__ void store_rows(const float* o_lds, const OutView& out, int b, int h,
+                                           int tok0, int rows_valid, const float* oc_row,
+                                           const AlphaView& alpha) {
+  const int lane = threadIdx.x & 63;
+  const int ch = lane & 15;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int r = (lane >> 4) + 4 * j;
+    if (r >= rows_valid) continue;
+    const int tok = tok0 + r;
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = o_lds[r * O_LDS_STRIDE + 8 * ch + e];
+    if (oc_row != nullptr) {
+      const floatx4 c0 = *reinterpret_cast<const floatx4*>(oc_row + 8 * ch);
+      const floatx4 c1 = *reinterpret_cast<const floatx4*>(oc_row + 8 * ch + 4);
+      if (alpha.p == nullptr || alpha.sd == 0) {
+        const float a = alpha_at(alpha, b, tok, h, 8 * ch);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) { v[e] = fmaf(a, c0[e], v[e]); v[4 + e] = fmaf(a, c1[e], v[4 + e]); }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          v[e] = fmaf(alpha_at(alpha, b, tok, h, 8 * ch + e), c0[e], v[e]);
+          v[4 + e] = fmaf(alpha_at(alpha, b, tok, h, 8 * ch + 4 + e), c1[e], v[4 + e]);
+        }
+      }
+    }
+    const int64_t off = (int64_t)b * out.sb + (int64_t)tok * out.ss + (int64_t)h * out.sh + 8 * ch;
+    if (out.dtype == ICSA_DT_BF16) {
+      *reinterpret_cast<bf16x8*>(reinterpret_cast<bf16*>(out.p) + off) = pack8_bf16(v);
+    } else {
+      float* dst = reinterpret_cast<float*>(out.p) + off;
+      *reinterpret_cast<floatx4*>(dst) = floatx4{v[0], v[1], v[2], v[3]};
+      *reinterpret_cast<floatx4*>(dst + 4) = floatx4{v[4], v[5], v[6], v[7]};
+    }
+  }
+}

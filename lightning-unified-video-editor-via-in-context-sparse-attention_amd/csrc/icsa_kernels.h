@@ -1,0 +1,112 @@
+// Parameter blocks and host launchers of every ICSA kernel (internal interface between
+// the kernel translation units and the C ABI in api.hip).
+#pragma once
+
+#include "icsa_common.h"
+
+// ---------------------------------------------------------------- stage 1 (pool.hip)
+struct PoolParams {
+  TokTensor x[3];       // inputs (p == nullptr -> skipped)
+  float* sums[3];       // [B, H, NB, D] fp32 block sums (nullptr -> skipped)
+  bf16* xb[3];          // bf16 copies, strides xb_* (nullptr -> skipped)
+  int64_t xb_sb, xb_ss, xb_sh;
+  bf16* vt;             // transposed copy of x[vt_src] (nullptr -> skipped)
+  int64_t vt_sb, vt_sh, vt_sd;
+  int vt_src;
+  int B, S, H, NB;      // S tokens, NB = ceil(S / 64) blocks
+};
+hipError_t launch_pool(const PoolParams& p, hipStream_t stream);
+
+// ---------------------------------------------------------------- stage 2 (compressed.hip)
+struct CompressedParams {
+  const float* qsum;    // [BH, NB, D]
+  const float* ksum;
+  const float* vsum;
+  float* P;             // [BH, NB, NB] logits, then softmax probabilities in place
+  float* out_c;         // [BH, NB, D]
+  float* sharp;         // [BH, NB]
+  int BH, NB, S;        // S: tokens (last block size = S - (NB-1)*64)
+  int n_t, k_sparsity;
+};
+hipError_t launch_compressed(const CompressedParams& p, hipStream_t stream);
+
+struct SelectParams {
+  const float* P;       // [BH, NB, NB]
+  const float* sharp;   // [BH, NB]
+  float* src_score;     // [BH, n_s]
+  int* sel;             // [BH, topK]   (ranked order)
+  int* order;           // [BH, NB]     (first n_peaked peaked, rest diffuse)
+  int* kvmap;           // [BH, NKV]    start block in the K/Vt source of new-KV block j, -1 zero
+  int BH, NB, n_t, n_s, topK, NKV;
+  int materialized;     // 1: new KV materialised in its own buffers (kvmap = identity)
+  int inject_sel, inject_order;   // 1: sel / order already hold caller decisions
+};
+hipError_t launch_select(const SelectParams& p, hipStream_t stream);
+
+struct NewKvSumsParams {
+  const float* ksum;    // [BH, Nsrc, D] source block sums
+  const float* vsum;
+  const int* kvmap;     // [BH, NKV]  source block index (token start / 64) or -1
+  int map_identity;     // 1: kvmap ignored, block j -> j
+  float* kc32;          // [BH, NKV, D]   fp32 sums of new-KV blocks
+  bf16* kc;             // [BH, NKVp, D]  bf16 sums (rows >= NKV zero)
+  bf16* vct;            // [BH, D, NKVp]  bf16 sums transposed, kv_slot() order
+  int BH, Nsrc, NKV, NKVp;
+};
+hipError_t launch_newkv_sums(const NewKvSumsParams& p, hipStream_t stream);
+
+struct Level3Params {
+  const float* qsum;    // [BH, NQsrc, D]
+  const int* rows;      // [BH, rows_stride] q-block list (nullptr -> identity)
+  int rows_offset, rows_stride;
+  const float* kc32;    // [BH, NKV, D]
+  int* idx;             // [BH, n_rows, top_k]  ascending block indices
+  int BH, NQsrc, n_rows, NKV, top_k;
+};
+hipError_t launch_level3(const Level3Params& p, hipStream_t stream);
+
+// ---------------------------------------------------------------- new-KV gather (gather.hip)
+struct GatherParams {
+  TokTensor k, v;       // [B, S, H, D]
+  const int* sel;       // [BH, topK]
+  bf16* kn;             // [BH, Tp, D]  row-major new K
+  bf16* vn;             // [BH, Tp, D]  row-major new V
+  int B, H, S, t, topK, Tkv, Tp;
+};
+hipError_t launch_gather(const GatherParams& p, hipStream_t stream);
+
+// ---------------------------------------------------------------- stage 3 (flash_attn.hip)
+struct FlashParams {
+  const bf16* q; int64_t q_sb, q_ss, q_sh;      // [B, Sq, H, D]
+  const bf16* k; int64_t k_sb, k_ss, k_sh;      // [B, Sk, H, D]
+  const bf16* vt; int64_t vt_sb, vt_sh, vt_sd;  // [B, H, D, Skp]
+  int B, H, Sq, Sk;
+  const int* qblocks; int qb_offset, qb_stride; int n_qblk;   // per-bh q-block list
+  int t_limit, n_tgt_tiles;        // KV tiles [0, n_tgt_tiles) of 64 keys, keys >= t_limit masked
+  const int* sel; int sel_stride; int n_sel; int sel_base;    // extra tiles at (sel_base + sel[r]) * 64
+  const float* out_c;              // [BH, NBq, D] residual (nullptr -> none)
+  int nb_q;
+  AlphaView alpha;
+  OutView out;
+  float scale_log2;                // log2(e) / sqrt(D)
+};
+hipError_t launch_flash(const FlashParams& p, hipStream_t stream);
+
+// ---------------------------------------------------------------- stage 4 (sparse_attn.hip)
+struct SparseParams {
+  const bf16* q; int64_t q_sb, q_ss, q_sh;      // [B, Sq, H, D]
+  const bf16* k; int64_t k_sb, k_st, k_sh;      // keys: b, token, h strides
+  const bf16* vt; int64_t vt_sb, vt_sh, vt_sd;  // [B, H, D, Tp]
+  int B, H, Sq, Sk;                  // Sk: tokens available in k/vt (rows >= Sk read as 0)
+  const int* qblocks; int qb_offset, qb_stride; int n_qblk;
+  const int* kvmap; int kvmap_identity;         // [BH, NKV] source block of new-KV block
+  const int* idx;                    // [BH, n_qblk, top_k] ascending
+  int top_k, NKV, NKVp;
+  const bf16* kc;                    // [BH, NKVp, D]
+  const bf16* vct;                   // [BH, D, NKVp]
+  const float* out_c; int nb_q;
+  AlphaView alpha;
+  OutView out;
+  float scale_log2;
+};
+hipError_t launch_sparse(const SparseParams& p, hipStream_t stream);

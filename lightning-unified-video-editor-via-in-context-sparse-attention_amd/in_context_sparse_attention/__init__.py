@@ -1,0 +1,32 @@
+"""MI355X (gfx950) in-context sparse attention -- the reference package's API with a HIP backend.
+
+Mirrors ``in_context_sparse_attention/__init__.py`` of the reference (``Backend``,
+``editing_sparse_attention``, ``editing_sparse_attention_tilelang``) and adds the kernel-host
+functions of the HIP backend.  Importing does not load the native library; the first GPU
+call does, and fails loudly if ``libicsa.so`` has not been built.
+"""
+from .editing_sparse_attention import (  # noqa: F401
+    Backend,
+    derived_sizes,
+    editing_sparse_attention,
+    editing_sparse_attention_tilelang,
+)
+from .hip_host import (  # noqa: F401
+    IcsaArgumentError,
+    flash_attn_func,
+    gather_kv,
+    pool,
+    sparse_piecewise_attn_1st_intervals,
+    sparse_piecewise_attn_1st_intervals_hip,
+)
+
+__all__ = [
+    'Backend',
+    'editing_sparse_attention',
+    'editing_sparse_attention_tilelang',
+    'sparse_piecewise_attn_1st_intervals_hip',
+    'sparse_piecewise_attn_1st_intervals',
+    'flash_attn_func',
+    'derived_sizes',
+    'IcsaArgumentError',
+]

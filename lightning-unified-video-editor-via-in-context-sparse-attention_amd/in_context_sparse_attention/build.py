@@ -1,0 +1,71 @@
+"""Build ``libicsa.so`` (gfx950) from ``../csrc`` with hipcc.
+
+Every HIP source is compiled to an object in ``csrc/_build`` (in parallel), then linked
+into ``in_context_sparse_attention/libicsa.so`` next to this file.  The link goes to a
+temporary name first and is renamed into place, so a concurrent loader never sees a
+half-written library.  Run ``python -m in_context_sparse_attention.build`` or call
+:func:`build_library`.
+"""
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+CSRC_DIR = os.path.join(os.path.dirname(PKG_DIR), "csrc")
+BUILD_DIR = os.path.join(CSRC_DIR, "_build")
+LIB_PATH = os.path.join(PKG_DIR, "libicsa.so")
+
+SOURCES = ["pool.hip", "compressed.hip", "gather.hip", "flash_attn.hip", "sparse_attn.hip", "api.hip"]
+
+HIP_FLAGS = [
+    "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
+    # packed fp32 VALU forms are kept out of every kernel
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wno-unused-command-line-argument",
+]
+
+
+def _hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc"):
+        if cand and os.path.exists(cand):
+            return cand
+    return "hipcc"
+
+
+def _run(cmd, verbose):
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    out = "\n".join(l for l in res.stdout.splitlines() if "packed-fp32-ops" not in l and
+                    "is not a recognized feature" not in l)
+    if res.returncode != 0:
+        raise RuntimeError(f"command failed ({res.returncode}): {' '.join(cmd)}\n{out}")
+    if verbose and out.strip():
+        print(out, flush=True)
+
+
+def build_library(verbose: bool = False, jobs: int = 8) -> str:
+    """Compile every HIP source for gfx950 and link libicsa.so; returns its path."""
+    os.makedirs(BUILD_DIR, exist_ok=True)
+    hipcc = _hipcc()
+    inc = ["-I", CSRC_DIR, "-I", os.path.join(os.path.dirname(os.path.dirname(PKG_DIR)), "include")]
+
+    def compile_one(src):
+        obj = os.path.join(BUILD_DIR, src.replace(".hip", ".o"))
+        _run([hipcc, *HIP_FLAGS, *inc, "-c", os.path.join(CSRC_DIR, src), "-o", obj], verbose)
+        return obj
+
+    with ThreadPoolExecutor(max_workers=max(1, min(jobs, len(SOURCES)))) as ex:
+        objs = list(ex.map(compile_one, SOURCES))
+    tmp = LIB_PATH + f".tmp{os.getpid()}"
+    _run([hipcc, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs], verbose)
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    path = build_library(verbose="-v" in sys.argv)
+    print(path)

@@ -1,0 +1,173 @@
+"""In-context sparse attention with the MI355X HIP backend.
+
+Mirror of the reference's ``in_context_sparse_attention/editing_sparse_attention.py``:
+``Backend`` (:25-34) gains ``HIP = 'hip'``, and ``editing_sparse_attention`` (:67-232) keeps
+its signature.  With ``backend='hip'`` the whole path -- pooling, compressed attention,
+per-head source retrieval, peaked/diffuse split, flash attention for the peaked blocks,
+sparse piecewise attention for the diffuse blocks, scatter and residual -- runs as one
+launch sequence of hand-written gfx950 kernels (libicsa.so) on the current stream; the
+concatenated new KV, the broadcast out_c and the gathered query halves are never built.
+
+The TileLang and Triton backends are CUDA-only and are not part of this build: naming
+them passes ``Backend.validate`` (they are valid names) but raises ``NotImplementedError``.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+from .hip_host import (BLOCK_M, IcsaArgumentError, _require, dtype_code, inner_contiguous,
+                       ptr, stream_ptr)
+
+
+class Backend:
+    """Sparse-attention backend constants (editing_sparse_attention.py:25-34 plus HIP)."""
+    TILELANG = 'tilelang'
+    TRITON = 'triton'
+    HIP = 'hip'
+
+    @classmethod
+    def validate(cls, backend: str) -> str:
+        if backend not in (cls.TILELANG, cls.TRITON, cls.HIP):
+            raise ValueError(
+                f"Unknown backend '{backend}'.  Valid: {cls.TILELANG}, {cls.TRITON}, {cls.HIP}")
+        return backend
+
+
+SIZE_NAMES = ["NB", "n_t", "n_s", "topK", "Tkv", "k_sparsity", "n_peaked", "n_diffuse",
+              "TKV_pad", "NKV", "top_k", "NKVp"]
+
+
+def derived_sizes(B, S, H, D, t_seq_len, sparsity=0.0625, srr=0.125, flat_ratio=0.5) -> dict:
+    """Derived sizes of one call, computed by the library (icsa_editing_sizes)."""
+    out = (ctypes.c_int32 * 12)()
+    rc = _lib.lib().icsa_editing_sizes(B, S, H, D, t_seq_len, float(sparsity), float(srr),
+                                       float(flat_ratio), ctypes.cast(out, ctypes.c_void_p))
+    _lib.check("icsa_editing_sizes", rc)
+    return dict(zip(SIZE_NAMES, list(out)))
+
+
+def _alpha_view(alpha_2, B, S, H, D, device):
+    """(tensor or None, scalar, dtype code, strides) of alpha_2 broadcast to [B, S, H, D]."""
+    if not isinstance(alpha_2, torch.Tensor):
+        return None, float(alpha_2), _lib.F32, (0, 0, 0, 0)
+    a = alpha_2
+    if a.dtype not in (torch.float32, torch.bfloat16):
+        a = a.float()
+    a = a.to(device)
+    _require(a.dim() <= 4, "alpha_2 must broadcast to [B, S, H, D]")
+    a = a.expand(B, S, H, D)
+    return a, 0.0, dtype_code(a), tuple(a.stride())
+
+
+@torch.no_grad()
+def _editing_sparse_attention_hip(q, k, v, t_seq_len, alpha_2=1.0, SPARSITY_RATIO=0.0625,
+                                  srr=0.125, flat_ratio=0.5, inject=None, keep_workspace=False):
+    """Runs the fused HIP path; returns ``(x, workspace_views or None)``."""
+    _require(q.is_cuda and k.is_cuda and v.is_cuda, "q, k, v must be on the GPU")
+    _require(q.ndim == 4 and q.shape == k.shape == v.shape, "q, k, v must be [B, S, H, D]")
+    B, S, H, D = q.shape
+    _require(0 <= t_seq_len <= S, f"t_seq_len {t_seq_len} outside [0, {S}]")
+    q, k, v = inner_contiguous(q), inner_contiguous(k), inner_contiguous(v)
+    for t in (q, k, v):
+        dtype_code(t)
+    L = _lib.lib()
+    sizes = derived_sizes(B, S, H, D, t_seq_len, SPARSITY_RATIO, srr, flat_ratio)
+    offs = (ctypes.c_int64 * len(_lib.WS_SLOTS))()
+    ws_bytes = L.icsa_editing_workspace_layout(B, S, H, D, t_seq_len, float(SPARSITY_RATIO),
+                                               float(srr), float(flat_ratio), dtype_code(q),
+                                               dtype_code(k), ctypes.cast(offs, ctypes.c_void_p))
+    if ws_bytes < 0:
+        raise _lib.IcsaError("icsa_editing_workspace_layout", int(ws_bytes))
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
+    out = torch.empty(B, S, H, D, dtype=q.dtype, device=q.device)
+    a, a_scalar, a_dt, a_st = _alpha_view(alpha_2, B, S, H, D, q.device)
+    inject = inject or {}
+    inj = {}
+    for name, shape in (("sel", (B, H, sizes["topK"])), ("order", (B, H, sizes["NB"])),
+                        ("l3", (B, H, sizes["n_diffuse"], sizes["top_k"]))):
+        if inject.get(name) is not None:
+            t = inject[name].to(device=q.device, dtype=torch.int32).contiguous()
+            _require(tuple(t.shape) == shape, f"inject[{name!r}] must have shape {shape}")
+            inj[name] = t
+    rc = L.icsa_editing_sparse_attention(
+        ptr(q), dtype_code(q), q.stride(0), q.stride(1), q.stride(2),
+        ptr(k), dtype_code(k), k.stride(0), k.stride(1), k.stride(2),
+        ptr(v), dtype_code(v), v.stride(0), v.stride(1), v.stride(2),
+        B, S, H, D, int(t_seq_len), float(SPARSITY_RATIO), float(srr), float(flat_ratio),
+        ptr(a), a_dt, a_st[0], a_st[1], a_st[2], a_st[3], float(a_scalar),
+        ptr(out), dtype_code(out), out.stride(0), out.stride(1), out.stride(2),
+        ptr(inj.get("sel")), ptr(inj.get("order")), ptr(inj.get("l3")),
+        ptr(ws), ws_bytes, stream_ptr(q.device))
+    _lib.check("icsa_editing_sparse_attention", rc)
+    if not keep_workspace:
+        return out, None
+    return out, workspace_views(ws, list(offs), sizes, B, H, D)
+
+
+def workspace_views(ws: torch.Tensor, offs, sizes: dict, B: int, H: int, D: int) -> dict:
+    """Typed views of the intermediate buffers (decisions, scores) of one call."""
+    z = sizes
+
+    def view(slot, dtype, shape):
+        off = offs[_lib.WS_SLOTS.index(slot)]
+        n = 1
+        for s in shape:
+            n *= s
+        nbytes = n * torch.empty(0, dtype=dtype).element_size()
+        return ws[off:off + nbytes].view(dtype).view(*shape)
+
+    NB = z["NB"]
+    return dict(
+        sizes=z,
+        q_sums=view("QSUM", torch.float32, (B, H, NB, D)),
+        k_sums=view("KSUM", torch.float32, (B, H, NB, D)),
+        v_sums=view("VSUM", torch.float32, (B, H, NB, D)),
+        P=view("P", torch.float32, (B, H, NB, NB)),
+        out_c=view("OUTC", torch.float32, (B, H, NB, D)),
+        sharpness=view("SHARP", torch.float32, (B, H, NB)),
+        src_score=view("SRCSCORE", torch.float32, (B, H, max(z["n_s"], 1))),
+        sel=view("SEL", torch.int32, (B, H, max(z["topK"], 1)))[..., :z["topK"]],
+        order=view("ORDER", torch.int32, (B, H, NB)),
+        kvmap=view("KVMAP", torch.int32, (B, H, z["NKV"])),
+        kc32=view("KC32", torch.float32, (B, H, z["NKV"], D)),
+        l3=view("L3", torch.int32, (B, H, max(z["n_diffuse"], 1), z["top_k"]))[:, :, :z["n_diffuse"]],
+    )
+
+
+def editing_sparse_attention(q, k, v, t_seq_len, s_seq_len, alpha_2=1.0, alpha_3=1.0,
+                             SPARSITY_RATIO=0.0625, backend=Backend.HIP, *, srr=0.125,
+                             flat_ratio=0.5):
+    """Editing sparse attention (reference: editing_sparse_attention.py:67-232).
+
+    Args:
+        q, k, v: [B, S, H, D] (bfloat16 or float32 each; D = 128), target tokens first
+        t_seq_len: target-video token count
+        s_seq_len: source-video token count (unused, as in the reference)
+        alpha_2: residual weight of the compressed-attention shortcut (float or tensor
+            broadcastable to [B, S, H, D])
+        alpha_3: unused (API compatibility)
+        SPARSITY_RATIO: fraction of KV blocks for the exact top-k (also sets k_sparsity)
+        backend: 'hip' (this build); 'tilelang' / 'triton' raise NotImplementedError
+        srr: source retrieval ratio (reference: 1/8, ``n_s // 8``)
+        flat_ratio: fraction of query blocks given exact attention (reference: 1/2)
+
+    Returns:
+        x: [B, S, H, D] in q.dtype
+    """
+    backend = Backend.validate(backend)
+    if backend != Backend.HIP:
+        raise NotImplementedError(
+            f"backend '{backend}' is CUDA-only and not part of this MI355X build; use 'hip'")
+    x, _ = _editing_sparse_attention_hip(q, k, v, t_seq_len, alpha_2, SPARSITY_RATIO, srr,
+                                         flat_ratio)
+    return x
+
+
+# Backward-compatible alias of the reference (there: always tilelang; here: the HIP path).
+editing_sparse_attention_tilelang = editing_sparse_attention
+
+__all__ = ["Backend", "editing_sparse_attention", "editing_sparse_attention_tilelang",
+           "derived_sizes", "IcsaArgumentError"]

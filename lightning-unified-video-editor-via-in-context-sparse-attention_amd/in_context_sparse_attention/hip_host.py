@@ -1,0 +1,197 @@
+"""HIP host functions with the reference's kernel-host signatures.
+
+* :func:`sparse_piecewise_attn_1st_intervals_hip` mirrors
+  ``sparse_piecewise_attn_1st_intervals_tilelang`` (tilelang_host.py:229-274) and the Triton
+  ``sparse_piecewise_attn_1st_intervals`` (triton_host.py:11-30): same arguments, shapes,
+  dtypes, return value and ownership.  Argument checks raise :class:`IcsaArgumentError`, an
+  ``AssertionError`` (what the reference's asserts raise) that is also a ``ValueError``.
+* :func:`flash_attn_func` mirrors the call made at editing_sparse_attention.py:211-215
+  (flash-attn's ``flash_attn_func(q, k, v)``, dense non-causal, default scale).
+* :func:`pool` and :func:`gather_kv` expose stage 1 and the new-KV gather.
+
+Work is enqueued on ``torch.cuda.current_stream()``; scratch memory comes from torch's
+caching allocator and is passed to the library as its workspace.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+
+BLOCK_M = 64
+
+
+class IcsaArgumentError(AssertionError, ValueError):
+    """Invalid argument (the reference raises AssertionError for the same conditions)."""
+
+
+def _require(cond: bool, msg: str) -> None:
+    if not cond:
+        raise IcsaArgumentError(msg)
+
+
+def dtype_code(t: torch.Tensor) -> int:
+    if t.dtype == torch.bfloat16:
+        return _lib.BF16
+    if t.dtype == torch.float32:
+        return _lib.F32
+    raise TypeError(f"unsupported dtype {t.dtype}: the HIP backend takes bfloat16 or float32")
+
+
+def inner_contiguous(t: torch.Tensor) -> torch.Tensor:
+    """The library needs a unit stride on the last dim and 16-byte aligned rows."""
+    es = t.element_size()
+    ok = t.stride(-1) == 1 and t.data_ptr() % 16 == 0 and all(
+        (s * es) % 16 == 0 for s in t.stride()[:-1])
+    return t if ok else t.contiguous()
+
+
+def stream_ptr(device: torch.device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
+
+
+@torch.no_grad()
+def sparse_piecewise_attn_1st_intervals_hip(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                                            sparsity: float = 0.1, block_size: int = 64, *,
+                                            indices: torch.Tensor = None,
+                                            return_indices: bool = False):
+    """Sparse piecewise attention (first-order intervals) on MI355X.
+
+    Args:
+        q: [B, H, TQ, D] bfloat16 (TQ multiple of 64)
+        k: [B, H, TKV, D] bfloat16 (TKV multiple of 64)
+        v: [B, H, TKV, D] bfloat16 (Vdim == D == 128)
+        sparsity: fraction of KV blocks attended exactly (top_k = max(1, int(sparsity*NKV)))
+        block_size: must be 64
+        indices: optional [B, H, TQ/64, top_k] int32 block lists (ascending) to use instead
+            of the kernel's own top-k (testing hook; not in the reference signature)
+        return_indices: also return the block lists used
+
+    Returns:
+        out: [B, H, TQ, D] bfloat16 (a new tensor owned by the caller)
+    """
+    _require(q.dtype == k.dtype == v.dtype == torch.bfloat16, "q, k, v must be bfloat16")
+    _require(q.is_cuda and k.is_cuda and v.is_cuda, "q, k, v must be on the GPU")
+    _require(block_size == 64, "Only block_size=64 supported.")
+    _require(q.ndim == 4 and k.ndim == 4 and v.ndim == 4, "q, k, v must be 4-D [B, H, T, D]")
+    _require(q.shape[0] == k.shape[0] == v.shape[0], "batch mismatch")
+    _require(q.shape[1] == k.shape[1] == v.shape[1], "head mismatch")
+    _require(q.shape[3] == k.shape[3], "Kdim must match between q and k")
+    _require(k.shape[2] == v.shape[2], "TKV must match between k and v")
+    _require(v.shape[3] == q.shape[3], "This entrypoint assumes Vdim == D (so VBlocks==1).")
+    B, H, TQ, D = q.shape
+    TKV = k.shape[2]
+    _require(TQ % BLOCK_M == 0 and TKV % BLOCK_M == 0, "TQ/TKV must be divisible by BT")
+    q, k, v = inner_contiguous(q), inner_contiguous(k), inner_contiguous(v)
+    L = _lib.lib()
+    NQ, NKV = TQ // BLOCK_M, TKV // BLOCK_M
+    top_k = max(1, int(sparsity * NKV))
+    out = torch.empty(B, H, TQ, D, dtype=torch.bfloat16, device=q.device)
+    ws_bytes = L.icsa_sparse_piecewise_workspace_size(B, H, TQ, TKV, D, float(sparsity))
+    if ws_bytes < 0:
+        raise _lib.IcsaError("icsa_sparse_piecewise_workspace_size", int(ws_bytes))
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
+    inj = None
+    if indices is not None:
+        inj = indices.to(device=q.device, dtype=torch.int32).contiguous()
+        _require(tuple(inj.shape) == (B, H, NQ, top_k), f"indices must be [B, H, {NQ}, {top_k}]")
+    idx_out = torch.empty(B, H, NQ, top_k, dtype=torch.int32, device=q.device) if return_indices else None
+    rc = L.icsa_sparse_piecewise_attn(
+        ptr(q), q.stride(0), q.stride(1), q.stride(2),
+        ptr(k), k.stride(0), k.stride(1), k.stride(2),
+        ptr(v), v.stride(0), v.stride(1), v.stride(2),
+        B, H, TQ, TKV, D, float(sparsity),
+        ptr(inj), ptr(idx_out),
+        ptr(out), out.stride(0), out.stride(1), out.stride(2),
+        ptr(ws), ws_bytes, stream_ptr(q.device))
+    _lib.check("icsa_sparse_piecewise_attn", rc)
+    return (out, idx_out) if return_indices else out
+
+
+# the Triton host's name (triton_host.py:11) for callers that import it directly
+sparse_piecewise_attn_1st_intervals = sparse_piecewise_attn_1st_intervals_hip
+
+
+@torch.no_grad()
+def flash_attn_func(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, dropout_p: float = 0.0,
+                    softmax_scale=None, causal: bool = False, out_dtype=None) -> torch.Tensor:
+    """Dense non-causal attention, ``[B, S, H, D]`` layout (flash-attn's ``flash_attn_func``
+    as called at editing_sparse_attention.py:211-215).  bf16 inputs; output bf16 unless
+    ``out_dtype=torch.float32``."""
+    _require(dropout_p == 0.0 and softmax_scale is None and not causal,
+             "only dropout_p=0, default softmax_scale and causal=False are supported")
+    _require(q.dtype == k.dtype == v.dtype == torch.bfloat16, "q, k, v must be bfloat16")
+    _require(q.is_cuda and k.is_cuda and v.is_cuda, "q, k, v must be on the GPU")
+    _require(q.ndim == 4 and k.shape == v.shape and q.shape[0] == k.shape[0] and
+             q.shape[2:] == k.shape[2:], "q [B,Sq,H,D], k/v [B,Sk,H,D] expected")
+    q, k, v = inner_contiguous(q), inner_contiguous(k), inner_contiguous(v)
+    B, Sq, H, D = q.shape
+    Sk = k.shape[1]
+    out_dtype = out_dtype or torch.bfloat16
+    out = torch.empty(B, Sq, H, D, dtype=out_dtype, device=q.device)
+    L = _lib.lib()
+    ws_bytes = L.icsa_flash_attn_workspace_size(B, Sk, H, D)
+    if ws_bytes < 0:
+        raise _lib.IcsaError("icsa_flash_attn_workspace_size", int(ws_bytes))
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
+    rc = L.icsa_flash_attn(
+        ptr(q), q.stride(0), q.stride(1), q.stride(2),
+        ptr(k), k.stride(0), k.stride(1), k.stride(2),
+        ptr(v), v.stride(0), v.stride(1), v.stride(2),
+        B, Sq, Sk, H, D,
+        ptr(out), dtype_code(out), out.stride(0), out.stride(1), out.stride(2),
+        ptr(ws), ws_bytes, stream_ptr(q.device))
+    _lib.check("icsa_flash_attn", rc)
+    return out
+
+
+@torch.no_grad()
+def pool(q=None, k=None, v=None, want_vt: bool = False):
+    """Stage 1: fp32 block sums ``[B, H, NB, D]`` of each given ``[B, S, H, D]`` tensor (None
+    for absent ones) and, with ``want_vt``, V transposed ``[B, H, D, NB*64]`` bf16."""
+    ref = next(t for t in (q, k, v) if t is not None)
+    B, S, H, D = ref.shape
+    NB = (S + BLOCK_M - 1) // BLOCK_M
+    ts = [inner_contiguous(t) if t is not None else None for t in (q, k, v)]
+    sums = [torch.empty(B, H, NB, D, dtype=torch.float32, device=ref.device) if t is not None else None
+            for t in ts]
+    vt = None
+    if want_vt:
+        _require(v is not None, "want_vt needs v")
+        vt = torch.empty(B, H, D, NB * BLOCK_M, dtype=torch.bfloat16, device=ref.device)
+    args = []
+    for t in ts:
+        if t is None:
+            args += [ctypes.c_void_p(0), 0, 0, 0, 0]
+        else:
+            args += [ptr(t), dtype_code(t), t.stride(0), t.stride(1), t.stride(2)]
+    rc = _lib.lib().icsa_pool(*args, B, S, H, D, ptr(sums[0]), ptr(sums[1]), ptr(sums[2]), ptr(vt),
+                              stream_ptr(ref.device))
+    _lib.check("icsa_pool", rc)
+    return sums[0], sums[1], sums[2], vt
+
+
+@torch.no_grad()
+def gather_kv(k: torch.Tensor, v: torch.Tensor, t_seq_len: int, sel: torch.Tensor):
+    """Materialised new KV ``[B, H, Tp, D]`` bf16 (editing_sparse_attention.py:138-159, zero
+    padded to a multiple of 64 rows)."""
+    k, v = inner_contiguous(k), inner_contiguous(v)
+    B, S, H, D = k.shape
+    topK = sel.shape[-1]
+    sel32 = sel.to(device=k.device, dtype=torch.int32).reshape(B * H, topK).contiguous()
+    Tkv = t_seq_len + topK * BLOCK_M
+    Tp = (Tkv + BLOCK_M - 1) // BLOCK_M * BLOCK_M
+    kn = torch.empty(B, H, Tp, D, dtype=torch.bfloat16, device=k.device)
+    vn = torch.empty_like(kn)
+    rc = _lib.lib().icsa_gather_kv(
+        ptr(k), dtype_code(k), k.stride(0), k.stride(1), k.stride(2),
+        ptr(v), dtype_code(v), v.stride(0), v.stride(1), v.stride(2),
+        B, S, H, D, t_seq_len, ptr(sel32), topK, ptr(kn), ptr(vn), stream_ptr(k.device))
+    _lib.check("icsa_gather_kv", rc)
+    return kn, vn

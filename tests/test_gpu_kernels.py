@@ -1,0 +1,110 @@
+"""GPU parity of the individual entry points (pool, flash attention, sparse host function)."""
+import math
+
+import pytest
+import torch
+
+import oracle as O
+from in_context_sparse_attention import (flash_attn_func, gather_kv, pool,
+                                         sparse_piecewise_attn_1st_intervals_hip)
+from in_context_sparse_attention.hip_host import IcsaArgumentError
+from parity import GAP, compare_out, l3_scale
+
+pytestmark = pytest.mark.gpu
+
+
+def _bf16(*shape, seed=0, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g) * scale).to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("S", [64, 1000, 4096])
+def test_pool_sums_and_transposed_v(gpu, S):
+    print(f"[case] pool S={S}", flush=True)
+    q, k, v = _bf16(2, S, 3, 128, seed=1), _bf16(2, S, 3, 128, seed=2), _bf16(2, S, 3, 128, seed=3)
+    qs, ks, vs, vt = pool(q.to(gpu), k.to(gpu), v.to(gpu), want_vt=True)
+    for x, s in ((q, qs), (k, ks), (v, vs)):
+        ref, _ = O.pool_blocks(x)
+        assert torch.allclose(s.cpu().double(), ref, rtol=1e-6, atol=1e-5)
+    # V^T: token tok of block-group g stored at slot kv_slot(tok)
+    NB = (S + 63) // 64
+    vp = torch.zeros(2, NB * 64, 3, 128, dtype=torch.bfloat16)
+    vp[:, :S] = v
+    tok = torch.arange(NB * 64)
+    slot = (tok & ~12) | ((tok & 4) << 1) | ((tok & 8) >> 1)
+    expect = torch.empty(2, 3, 128, NB * 64, dtype=torch.bfloat16)
+    expect[..., slot] = vp.permute(0, 2, 3, 1)
+    assert torch.equal(vt.cpu(), expect)
+
+
+@pytest.mark.parametrize("Sq,Sk,H", [(64, 64, 1), (200, 300, 2), (4096, 4096, 2), (130, 4160, 3)])
+def test_flash_attn_dense(gpu, Sq, Sk, H):
+    print(f"[case] flash Sq={Sq} Sk={Sk} H={H}", flush=True)
+    q, k, v = _bf16(1, Sq, H, 128, seed=4), _bf16(1, Sk, H, 128, seed=5), _bf16(1, Sk, H, 128, seed=6)
+    out = flash_attn_func(q.to(gpu), k.to(gpu), v.to(gpu), out_dtype=torch.float32)
+    ref = O.dense_attention(q.double().permute(0, 2, 1, 3), k.double().permute(0, 2, 1, 3),
+                            v.double().permute(0, 2, 1, 3)).permute(0, 2, 1, 3)
+    compare_out(out, ref)
+
+
+def test_flash_attn_large_logits(gpu):
+    # peaked softmax: logits up to ~40 exercise the running-max rescale path
+    q, k, v = _bf16(1, 512, 2, 128, seed=7, scale=3.0), _bf16(1, 1024, 2, 128, seed=8, scale=3.0), \
+        _bf16(1, 1024, 2, 128, seed=9)
+    out = flash_attn_func(q.to(gpu), k.to(gpu), v.to(gpu), out_dtype=torch.float32)
+    ref = O.dense_attention(q.double().permute(0, 2, 1, 3), k.double().permute(0, 2, 1, 3),
+                            v.double().permute(0, 2, 1, 3)).permute(0, 2, 1, 3)
+    compare_out(out, ref)
+
+
+@pytest.mark.parametrize("TQ,TKV,sparsity", [(512, 1024, 0.25), (1024, 4608, 0.0625), (256, 8192, 0.0625)])
+def test_sparse_piecewise_host(gpu, TQ, TKV, sparsity):
+    print(f"[case] sparse TQ={TQ} TKV={TKV} sparsity={sparsity}", flush=True)
+    q, k, v = _bf16(1, 2, TQ, 128, seed=10), _bf16(1, 2, TKV, 128, seed=11), _bf16(1, 2, TKV, 128, seed=12)
+    out, idx = sparse_piecewise_attn_1st_intervals_hip(q.to(gpu), k.to(gpu), v.to(gpu), sparsity,
+                                                       return_indices=True)
+    ref, ref_idx, scores = O.sparse_piecewise_attn(q, k, v, sparsity, indices=idx.long().cpu())
+    top_k = idx.shape[-1]
+    assert O.check_topk_valid(scores / l3_scale(128), idx.long().cpu(), top_k, GAP, ordered=False).all()
+    compare_out(out, ref)
+
+
+def test_sparse_piecewise_quirk_case(gpu):
+    # Keys of a late chunk align with the queries: the interval's running max rises after
+    # earlier chunks were accumulated, which the reference does not rescale.  The oracle
+    # reproduces that; an implementation that rescaled g_acc / g_l would differ here.
+    TQ, TKV = 64, 64 * 192
+    q = _bf16(1, 1, TQ, 128, seed=13)
+    k = _bf16(1, 1, TKV, 128, seed=14, scale=0.2)
+    # block 150 (chunk 2) holds 64 copies of 20 x the mean query: its interval score dwarfs
+    # every exact logit, so chunks 0-1 stay weighted by the stale running max
+    k[0, 0, 64 * 150:64 * 151] = (20.0 * q[0, 0].float().mean(0)).expand(64, 128).to(torch.bfloat16)
+    v = _bf16(1, 1, TKV, 128, seed=15)
+    idx = torch.arange(12, dtype=torch.int32).view(1, 1, 1, 12)
+    out = sparse_piecewise_attn_1st_intervals_hip(q.to(gpu), k.to(gpu), v.to(gpu), 0.0625,
+                                                  indices=idx.to(gpu))
+    ref, _, _ = O.sparse_piecewise_attn(q, k, v, 0.0625, indices=idx.long())
+    compare_out(out, ref)
+
+
+def test_gather_kv_matches_token_map(gpu):
+    k, v = _bf16(1, 1000, 2, 128, seed=16), _bf16(1, 1000, 2, 128, seed=17)
+    t = 500
+    sel = torch.tensor([[[7, 0, 3], [1, 2, 6]]])            # n_t = 7 -> blocks 7+sel (block 15 partial)
+    kn, vn = gather_kv(k.to(gpu), v.to(gpu), t, sel)
+    tokmap = O.new_kv_token_map(t, 1000, sel)
+    ref_k = O.gather_new_kv(k, tokmap, torch.float32).to(torch.bfloat16)
+    ref_v = O.gather_new_kv(v, tokmap, torch.float32).to(torch.bfloat16)
+    Tkv = ref_k.shape[2]
+    assert torch.equal(kn[:, :, :Tkv].cpu(), ref_k) and torch.equal(vn[:, :, :Tkv].cpu(), ref_v)
+    assert (kn[:, :, Tkv:] == 0).all()
+
+
+def test_argument_errors_mirror_reference(gpu):
+    q = torch.zeros(1, 1, 64, 128, dtype=torch.bfloat16, device=gpu)
+    with pytest.raises(AssertionError):
+        sparse_piecewise_attn_1st_intervals_hip(q, q, q, block_size=32)
+    with pytest.raises(IcsaArgumentError):
+        sparse_piecewise_attn_1st_intervals_hip(q.float(), q, q)
+    with pytest.raises(IcsaArgumentError):
+        sparse_piecewise_attn_1st_intervals_hip(q[:, :, :60], q, q)
