@@ -1,0 +1,246 @@
+#!/usr/bin/env python3
+"""Benchmark of the in-context sparse attention layer on one MI355X.
+
+Workload: B=1, H=40, D=128, 65,536 tokens (target 32,760 + 8 pad,
+source 32,760 + 8 pad), Q/K/V ~ N(0,1) with target K/V = source K/V + 0.3 N(0,1), bf16,
+SPARSITY_RATIO (SAR) 0.0625, SRR 1/8, flat ratio 0.5.  Synthetic data, inputs resident in
+HBM before the timed region.
+
+One step = one call of the fused HIP path (``editing_sparse_attention(..., backend='hip')``,
+every stage from the bf16 [B, S, H, D] inputs to the [B, S, H, D] output).  Reported:
+
+* value          dense-equivalent TFLOP/s = 4 B H S^2 D / layer time (the metric's
+                 "effective TFLOP/s"); ``ms_per_step`` is the layer latency.
+* executed       algorithmic FLOPs actually needed by the sparse path / layer time.
+* dense_fa       this library's dense bf16 flash attention at the same shape (the speedup
+                 denominator), timed in the same run.
+* stage_ms       per-stage times from HIP events recorded by the library on its stream
+                 inside the timed steps.
+* roofline       the dominant kernel (peaked-block flash attention): algorithmic FLOPs per
+                 launch / its event-timed duration vs the 2.5 PFLOP/s bf16 dense MFMA peak.
+* cpu_baseline   the CPU oracle (PyTorch eager fp32, this repo's restatement of the
+                 reference path) on config 1, timed on the host cores of this box.
+
+``--gpus N`` with N > 1 exits: this build measures one GPU (heads shard across GPUs with no
+communication inside the op).
+"""
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG_PARENT = os.path.join(ROOT, "lightning-unified-video-editor-via-in-context-sparse-attention_amd")
+for _p in (ROOT, PKG_PARENT):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+PEAK_BF16_TFLOPS = 2500.0
+PEAK_HBM_GBPS = 8000.0
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def load_traffic(path):
+    """HBM bytes per launch of the dominant kernel from a committed rocprofv3 summary
+    (line ``traffic_bytes_per_launch: N``), or None."""
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.strip().startswith("traffic_bytes_per_launch:"):
+                    return float(line.split(":", 1)[1])
+    except OSError:
+        return None
+    return None
+
+
+def cpu_baseline(seconds):
+    import torch
+    import oracle as O
+    from in_context_sparse_attention.synthetic import config_inputs
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except AttributeError:
+        cores = os.cpu_count() or 1
+    cores = max(1, min(cores, 16))
+    torch.set_num_threads(cores)
+    q, k, v, t = config_inputs(1)
+    B, S, H, D = q.shape
+    q32, k32, v32 = q.float(), k.float(), v.float()
+    times = []
+    t_start = time.perf_counter()
+    while True:
+        t0 = time.perf_counter()
+        O.editing_sparse_attention(q32, k32, v32, t, S - t, alpha_2=1.0, dtype=torch.float32)
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() - t_start >= seconds and len(times) >= 3:
+            break
+    med = statistics.median(times)
+    dense_flops = 4.0 * B * H * S * S * D
+    return {
+        "value": dense_flops / med / 1e12,
+        "unit": "TFLOP/s (dense-equivalent)",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"config 1 (B=1, H=2, S=8192, D=128) whole path in fp32, {len(times)} runs, "
+                   f"median {med * 1e3:.1f} ms"),
+        "ms_median": med * 1e3,
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", type=int, default=2, choices=[2, 3])
+    ap.add_argument("--sar", type=float, default=0.0625)
+    ap.add_argument("--flat-ratio", type=float, default=0.5)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-dense", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures a single GPU; --gpus {args.gpus} is not supported by this build "
+              "(heads shard across GPUs without communication, see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from in_context_sparse_attention import _lib, flash_attn_func, gather_kv
+    from in_context_sparse_attention.editing_sparse_attention import (
+        _editing_sparse_attention_hip, derived_sizes)
+    from in_context_sparse_attention.synthetic import config_inputs
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    _lib.lib()
+    q, k, v, t = config_inputs(args.config, device=dev)
+    B, S, H, D = q.shape
+    z = derived_sizes(B, S, H, D, t, args.sar, 0.125, args.flat_ratio)
+    log(f"[bench] config {args.config}: B={B} S={S} H={H} D={D} t={t} sizes={z}")
+
+    def step(events=None):
+        return _editing_sparse_attention_hip(q, k, v, t, 1.0, args.sar, 0.125, args.flat_ratio,
+                                             stage_events=events)[0]
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in _lib.STAGES] for _ in range(args.steps)]
+    for row in ev:
+        for e in row:
+            e.record(stream)           # materialise the events before the library re-records them
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(ev[i])
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_step = wall * 1e3 / args.steps
+    stage_ms = {}
+    for si in range(1, len(_lib.STAGES)):
+        vals = [ev[i][si - 1].elapsed_time(ev[i][si]) for i in range(args.steps)]
+        stage_ms[_lib.STAGES[si]] = statistics.mean(vals)
+    log(f"[bench] layer {ms_per_step:.3f} ms/step; stages (ms): "
+        + ", ".join(f"{n}={v:.3f}" for n, v in stage_ms.items()))
+
+    dense_flops = 4.0 * B * H * S * S * D
+    fa_flops = 4.0 * B * H * z["n_peaked"] * 64 * z["Tkv"] * D
+    sparse_flops = 4.0 * B * H * z["n_diffuse"] * 64 * (z["top_k"] * 64 + z["NKV"]) * D
+    comp_flops = 4.0 * B * H * z["NB"] * z["NB"] * D
+    exec_flops = fa_flops + sparse_flops + comp_flops
+
+    # stage 1 bytes: read q, k, v + write fp32 sums + write V^T; stage 2: read sums, write
+    # P once, write out_c (the algorithmic minimum of the compressed stage)
+    BH, NB, Sp = B * H, z["NB"], z["NB"] * 64
+    pool_bytes = 3 * B * S * H * D * 2 + 3 * BH * NB * D * 4 + BH * D * Sp * 2
+    comp_bytes = 3 * BH * NB * D * 4 + BH * NB * NB * 4 + BH * NB * D * 4
+
+    # KV gather (materialised new KV of the drop-in path) on this call's selection
+    out, views = _editing_sparse_attention_hip(q, k, v, t, 1.0, args.sar, 0.125, args.flat_ratio,
+                                               keep_workspace=True)
+    sel = views["sel"].clone()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    gather_kv(k, v, t, sel)
+    e0.record(stream)
+    for _ in range(5):
+        gather_kv(k, v, t, sel)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    gather_ms = e0.elapsed_time(e1) / 5
+    Tp = z["TKV_pad"]
+    gather_bytes = 2 * (BH * z["Tkv"] * D * 2) + 2 * (BH * Tp * D * 2)
+    del out, views
+
+    dense = None
+    if not args.no_dense:
+        for _ in range(2):
+            flash_attn_func(q, k, v)
+        torch.cuda.synchronize()
+        de = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(args.steps)]
+        for a, b in de:
+            a.record(stream)
+            flash_attn_func(q, k, v)
+            b.record(stream)
+        torch.cuda.synchronize()
+        dense_ms = statistics.mean(a.elapsed_time(b) for a, b in de)
+        dense = {"ms": dense_ms, "tflops": dense_flops / dense_ms / 1e9,
+                 "mfma_frac": dense_flops / dense_ms / 1e9 / PEAK_BF16_TFLOPS}
+        log(f"[bench] dense FA {dense_ms:.3f} ms ({dense['tflops']:.1f} TFLOP/s)")
+
+    fa_ms = stage_ms["flash"]
+    fa_tflops = fa_flops / fa_ms / 1e9
+    traffic = load_traffic(os.path.join(ROOT, "profiles", "flash_attn_peaked_cfg2.md"))
+    result = {
+        "metric": "sparse-attn layer ms + TFLOP/s at 65K tok H=40 D=128; speedup vs dense FA",
+        "value": dense_flops / ms_per_step / 1e9,
+        "unit": "TFLOP/s (dense-equivalent)",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) Q/K/V, target K/V = source + 0.3 N(0,1); no checkpoints)",
+        "config": {"workload": f"config {args.config}: one in-context sparse attention layer, "
+                               f"B={B} H={H} D={D} S={S} (t={t}), SAR={args.sar}, SRR=0.125, "
+                               f"flat={args.flat_ratio}",
+                   "global_batch": B, "seq_len": S, "parallelism": "single-gpu"},
+        "layer_ms": ms_per_step,
+        "executed_tflops": exec_flops / ms_per_step / 1e9,
+        "dense_fa": dense,
+        "speedup_vs_dense_fa": (dense["ms"] / ms_per_step) if dense else None,
+        "stage_ms": stage_ms,
+        "hbm_gbps": {
+            "pool": pool_bytes / stage_ms["pool"] / 1e6,
+            "compressed": comp_bytes / stage_ms["compressed"] / 1e6,
+            "kv_gather": gather_bytes / gather_ms / 1e6,
+        },
+        "mfma_frac": {"flash": fa_tflops / PEAK_BF16_TFLOPS,
+                      "sparse": sparse_flops / stage_ms["sparse"] / 1e9 / PEAK_BF16_TFLOPS},
+        "roofline": {"bound": "mfma", "achieved": fa_tflops, "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": fa_tflops / PEAK_BF16_TFLOPS,
+                     "traffic": traffic,
+                     "kernel": "icsa_flash_kernel (peaked query blocks)",
+                     "flops_per_launch": fa_flops},
+    }
+    if not args.no_cpu_baseline:
+        cb = cpu_baseline(args.cpu_seconds)
+        log(f"[bench] cpu baseline: {cb['sample']} on {cb['cores']} threads")
+        result["cpu_baseline"] = cb
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -112,6 +112,30 @@ int icsa_editing_sparse_attention(
     const int32_t* inject_sel, const int32_t* inject_order, const int32_t* inject_l3,
     void* workspace, int64_t workspace_bytes, void* stream);
 
+/* Stage boundaries recorded by icsa_editing_sparse_attention_ev (event index). */
+#define ICSA_STAGE_START 0      /* before stage 1                                   */
+#define ICSA_STAGE_POOL 1       /* after pooling (+ V transpose)                      */
+#define ICSA_STAGE_COMPRESSED 2 /* after compressed attention (logits, softmax, out_c) */
+#define ICSA_STAGE_SELECT 3     /* after retrieval, split, new-KV sums, level-3 top-k */
+#define ICSA_STAGE_SPARSE 4     /* after the sparse piecewise kernel (diffuse blocks)  */
+#define ICSA_STAGE_FLASH 5      /* after the flash-attention kernel (peaked blocks)    */
+#define ICSA_STAGE_COUNT 6
+
+/* Same as icsa_editing_sparse_attention, and records hipEvent_t stage_events[i]
+ * (ICSA_STAGE_COUNT created events) on the stream at each stage boundary, for profiling
+ * on the stream the kernels run on.  No synchronisation is added.  (No counterpart in the
+ * reference, which publishes no per-stage timing.) */
+int icsa_editing_sparse_attention_ev(
+    const void* q, int q_dtype, int64_t q_sb, int64_t q_ss, int64_t q_sh,
+    const void* k, int k_dtype, int64_t k_sb, int64_t k_ss, int64_t k_sh,
+    const void* v, int v_dtype, int64_t v_sb, int64_t v_ss, int64_t v_sh,
+    int B, int S, int H, int D, int t_seq_len, double sparsity, double srr, double flat_ratio,
+    const void* alpha, int alpha_dtype, int64_t a_sb, int64_t a_ss, int64_t a_sh, int64_t a_sd,
+    float alpha_scalar,
+    void* out, int out_dtype, int64_t o_sb, int64_t o_ss, int64_t o_sh,
+    const int32_t* inject_sel, const int32_t* inject_order, const int32_t* inject_l3,
+    void* workspace, int64_t workspace_bytes, void* stream, void* const* stage_events);
+
 /* Workspace bytes of icsa_sparse_piecewise_attn. */
 int64_t icsa_sparse_piecewise_workspace_size(int B, int H, int TQ, int TKV, int D, double sparsity);
 

@@ -174,16 +174,32 @@ int64_t icsa_editing_workspace_size(int B, int S, int H, int D, int t_seq_len, d
                                        k_dtype, nullptr);
 }
 
-int icsa_editing_sparse_attention(
-    const void* q, int q_dtype, int64_t q_sb, int64_t q_ss, int64_t q_sh,
-    const void* k, int k_dtype, int64_t k_sb, int64_t k_ss, int64_t k_sh,
-    const void* v, int v_dtype, int64_t v_sb, int64_t v_ss, int64_t v_sh,
-    int B, int S, int H, int D, int t_seq_len, double sparsity, double srr, double flat_ratio,
-    const void* alpha, int alpha_dtype, int64_t a_sb, int64_t a_ss, int64_t a_sh, int64_t a_sd,
-    float alpha_scalar,
-    void* out, int out_dtype, int64_t o_sb, int64_t o_ss, int64_t o_sh,
-    const int32_t* inject_sel, const int32_t* inject_order, const int32_t* inject_l3,
-    void* workspace, int64_t workspace_bytes, void* stream_) {
+}  // extern "C"
+
+namespace {
+
+#define ICSA_EDITING_ARGS                                                                    \
+    const void* q, int q_dtype, int64_t q_sb, int64_t q_ss, int64_t q_sh,                   \
+    const void* k, int k_dtype, int64_t k_sb, int64_t k_ss, int64_t k_sh,                   \
+    const void* v, int v_dtype, int64_t v_sb, int64_t v_ss, int64_t v_sh,                   \
+    int B, int S, int H, int D, int t_seq_len, double sparsity, double srr, double flat_ratio, \
+    const void* alpha, int alpha_dtype, int64_t a_sb, int64_t a_ss, int64_t a_sh, int64_t a_sd, \
+    float alpha_scalar,                                                                      \
+    void* out, int out_dtype, int64_t o_sb, int64_t o_ss, int64_t o_sh,                     \
+    const int32_t* inject_sel, const int32_t* inject_order, const int32_t* inject_l3,        \
+    void* workspace, int64_t workspace_bytes, void* stream_
+#define ICSA_EDITING_PASS                                                                    \
+    q, q_dtype, q_sb, q_ss, q_sh, k, k_dtype, k_sb, k_ss, k_sh, v, v_dtype, v_sb, v_ss, v_sh, \
+    B, S, H, D, t_seq_len, sparsity, srr, flat_ratio, alpha, alpha_dtype, a_sb, a_ss, a_sh,  \
+    a_sd, alpha_scalar, out, out_dtype, o_sb, o_ss, o_sh, inject_sel, inject_order,          \
+    inject_l3, workspace, workspace_bytes, stream_
+
+int editing_impl(ICSA_EDITING_ARGS, void* const* stage_events) {
+  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+  auto mark = [&](int i) -> hipError_t {
+    return stage_events ? hipEventRecord(reinterpret_cast<hipEvent_t>(stage_events[i]), stream)
+                        : hipSuccess;
+  };
   int rc = validate_common(B, S, H, D);
   if (rc) return rc;
   if ((rc = check_dtype(q_dtype, "q")) || (rc = check_dtype(k_dtype, "k")) ||
@@ -207,7 +223,6 @@ int icsa_editing_sparse_attention(
   if (workspace_bytes < L.total)
     return fail(ICSA_EWORKSPACE, "workspace %lld bytes < required %lld", (long long)workspace_bytes,
                 (long long)L.total);
-  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
   char* ws = reinterpret_cast<char*>(workspace);
   auto WS = [&](int slot) { return ws + L.off[slot]; };
   const int BH = B * H;
@@ -230,7 +245,9 @@ int icsa_editing_sparse_attention(
   pp.vt_sb = (int64_t)H * ICSA_D * Sp; pp.vt_sh = ICSA_D * Sp; pp.vt_sd = Sp;
   pp.vt_src = 2;
   pp.B = B; pp.S = S; pp.H = H; pp.NB = z.NB;
+  ICSA_HIP_TRY(mark(ICSA_STAGE_START), "event");
   ICSA_HIP_TRY(launch_pool(pp, stream), "pool");
+  ICSA_HIP_TRY(mark(ICSA_STAGE_POOL), "event");
 
   // bf16 views of q / k used by the attention kernels
   const bf16* qb = q_dtype == ICSA_BF16 ? reinterpret_cast<const bf16*>(q) : pp.xb[0];
@@ -250,6 +267,7 @@ int icsa_editing_sparse_attention(
   cp.sharp = reinterpret_cast<float*>(WS(ICSA_WS_SHARP));
   cp.BH = BH; cp.NB = z.NB; cp.S = S; cp.n_t = z.n_t; cp.k_sparsity = z.k_sparsity;
   ICSA_HIP_TRY(launch_compressed(cp, stream), "compressed attention");
+  ICSA_HIP_TRY(mark(ICSA_STAGE_COMPRESSED), "event");
 
   int32_t* sel = reinterpret_cast<int32_t*>(WS(ICSA_WS_SEL));
   int32_t* order = reinterpret_cast<int32_t*>(WS(ICSA_WS_ORDER));
@@ -332,6 +350,7 @@ int icsa_editing_sparse_attention(
     }
   }
 
+  ICSA_HIP_TRY(mark(ICSA_STAGE_SELECT), "event");
   const AlphaView av = make_alpha(alpha, alpha_dtype, a_sb, a_ss, a_sh, a_sd, alpha_scalar);
   OutView ov{out, o_sb, o_ss, o_sh, out_dtype};
   const float scale_log2 = kLog2e / std::sqrt((float)ICSA_D);
@@ -351,6 +370,7 @@ int icsa_editing_sparse_attention(
     s.alpha = av; s.out = ov; s.scale_log2 = scale_log2;
     ICSA_HIP_TRY(launch_sparse(s, stream), "sparse attention");
   }
+  ICSA_HIP_TRY(mark(ICSA_STAGE_SPARSE), "event");
 
   // ---- stage 3: flash attention on the peaked blocks ----
   if (z.n_peaked > 0) {
@@ -366,10 +386,25 @@ int icsa_editing_sparse_attention(
     f.alpha = av; f.out = ov; f.scale_log2 = scale_log2;
     ICSA_HIP_TRY(launch_flash(f, stream), "flash attention");
   }
+  ICSA_HIP_TRY(mark(ICSA_STAGE_FLASH), "event");
   return ICSA_OK;
 }
 
+}  // namespace
+
+extern "C" {
+
+int icsa_editing_sparse_attention(ICSA_EDITING_ARGS) {
+  return editing_impl(ICSA_EDITING_PASS, nullptr);
+}
+
+int icsa_editing_sparse_attention_ev(ICSA_EDITING_ARGS, void* const* stage_events) {
+  return editing_impl(ICSA_EDITING_PASS, stage_events);
+}
+
 // ---------------------------------------------------------------------------------------
+
+}  // extern "C"
 
 namespace {
 struct SpLayout {
@@ -394,6 +429,8 @@ SpLayout sparse_layout(int B, int H, int TQ, int TKV, double sparsity) {
   return L;
 }
 }  // namespace
+
+extern "C" {
 
 int64_t icsa_sparse_piecewise_workspace_size(int B, int H, int TQ, int TKV, int D, double sparsity) {
   if (B <= 0 || H <= 0 || TQ <= 0 || TKV <= 0 || D != ICSA_D) return -1;

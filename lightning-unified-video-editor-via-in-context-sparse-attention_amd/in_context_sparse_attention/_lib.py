@@ -24,13 +24,17 @@ EWORKSPACE = -3
 EHIP = -4
 
 # workspace slots of icsa_editing_sparse_attention (enum icsa_ws_slot)
+# stage boundaries of icsa_editing_sparse_attention_ev
+STAGES = ["start", "pool", "compressed", "select", "sparse", "flash"]
+
 WS_SLOTS = ["QSUM", "KSUM", "VSUM", "VT", "QB", "KB", "P", "OUTC", "SHARP", "SRCSCORE", "SEL",
             "ORDER", "KVMAP", "KC32", "KC", "VCT", "L3", "KN", "VN", "VTN", "NKSUM", "NVSUM"]
 
 # every symbol include/icsa.h declares
 EXPORTS = [
     "icsa_editing_sizes", "icsa_editing_workspace_size", "icsa_editing_workspace_layout",
-    "icsa_editing_sparse_attention", "icsa_sparse_piecewise_workspace_size",
+    "icsa_editing_sparse_attention", "icsa_editing_sparse_attention_ev",
+    "icsa_sparse_piecewise_workspace_size",
     "icsa_sparse_piecewise_attn", "icsa_flash_attn_workspace_size", "icsa_flash_attn",
     "icsa_pool", "icsa_gather_kv", "icsa_last_error", "icsa_version",
 ]
@@ -54,6 +58,15 @@ _SIGNATURES = {
         _p, _i, _l, _l, _l,
         _p, _p, _p,
         _p, _l, _p]),
+    "icsa_editing_sparse_attention_ev": (_i, [
+        _p, _i, _l, _l, _l,
+        _p, _i, _l, _l, _l,
+        _p, _i, _l, _l, _l,
+        _i, _i, _i, _i, _i, _d, _d, _d,
+        _p, _i, _l, _l, _l, _l, _f,
+        _p, _i, _l, _l, _l,
+        _p, _p, _p,
+        _p, _l, _p, _p]),
     "icsa_sparse_piecewise_workspace_size": (_l, [_i, _i, _i, _i, _i, _d]),
     "icsa_sparse_piecewise_attn": (_i, [
         _p, _l, _l, _l,

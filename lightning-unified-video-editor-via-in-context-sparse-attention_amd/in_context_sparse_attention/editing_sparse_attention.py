@@ -64,8 +64,13 @@ def _alpha_view(alpha_2, B, S, H, D, device):
 
 @torch.no_grad()
 def _editing_sparse_attention_hip(q, k, v, t_seq_len, alpha_2=1.0, SPARSITY_RATIO=0.0625,
-                                  srr=0.125, flat_ratio=0.5, inject=None, keep_workspace=False):
-    """Runs the fused HIP path; returns ``(x, workspace_views or None)``."""
+                                  srr=0.125, flat_ratio=0.5, inject=None, keep_workspace=False,
+                                  stage_events=None):
+    """Runs the fused HIP path; returns ``(x, workspace_views or None)``.
+
+    ``stage_events``: optional list of ``len(_lib.STAGES)`` recorded ``torch.cuda.Event``s
+    (enable_timing=True) that the library re-records at each stage boundary on the stream.
+    """
     _require(q.is_cuda and k.is_cuda and v.is_cuda, "q, k, v must be on the GPU")
     _require(q.ndim == 4 and q.shape == k.shape == v.shape, "q, k, v must be [B, S, H, D]")
     B, S, H, D = q.shape
@@ -92,7 +97,14 @@ def _editing_sparse_attention_hip(q, k, v, t_seq_len, alpha_2=1.0, SPARSITY_RATI
             t = inject[name].to(device=q.device, dtype=torch.int32).contiguous()
             _require(tuple(t.shape) == shape, f"inject[{name!r}] must have shape {shape}")
             inj[name] = t
-    rc = L.icsa_editing_sparse_attention(
+    ev_args = []
+    fn = L.icsa_editing_sparse_attention
+    if stage_events is not None:
+        _require(len(stage_events) == len(_lib.STAGES), "one event per stage boundary")
+        handles = (ctypes.c_void_p * len(stage_events))(*[e.cuda_event for e in stage_events])
+        ev_args = [ctypes.cast(handles, ctypes.c_void_p)]
+        fn = L.icsa_editing_sparse_attention_ev
+    rc = fn(
         ptr(q), dtype_code(q), q.stride(0), q.stride(1), q.stride(2),
         ptr(k), dtype_code(k), k.stride(0), k.stride(1), k.stride(2),
         ptr(v), dtype_code(v), v.stride(0), v.stride(1), v.stride(2),
@@ -100,7 +112,7 @@ def _editing_sparse_attention_hip(q, k, v, t_seq_len, alpha_2=1.0, SPARSITY_RATI
         ptr(a), a_dt, a_st[0], a_st[1], a_st[2], a_st[3], float(a_scalar),
         ptr(out), dtype_code(out), out.stride(0), out.stride(1), out.stride(2),
         ptr(inj.get("sel")), ptr(inj.get("order")), ptr(inj.get("l3")),
-        ptr(ws), ws_bytes, stream_ptr(q.device))
+        ptr(ws), ws_bytes, stream_ptr(q.device), *ev_args)
     _lib.check("icsa_editing_sparse_attention", rc)
     if not keep_workspace:
         return out, None
