@@ -10,7 +10,9 @@ import ctypes
 import os
 import threading
 
-_LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libicsa.so")
+# ICSA_LIB_PATH selects another build of the same library (e.g. a tuning variant)
+_LIB_PATH = os.environ.get("ICSA_LIB_PATH") or os.path.join(
+    os.path.dirname(os.path.abspath(__file__)), "libicsa.so")
 _lock = threading.Lock()
 _lib = None
 
@@ -23,10 +25,10 @@ EUNSUPPORTED = -2
 EWORKSPACE = -3
 EHIP = -4
 
-# workspace slots of icsa_editing_sparse_attention (enum icsa_ws_slot)
 # stage boundaries of icsa_editing_sparse_attention_ev
 STAGES = ["start", "pool", "compressed", "select", "sparse", "flash"]
 
+# workspace slots of icsa_editing_sparse_attention (enum icsa_ws_slot)
 WS_SLOTS = ["QSUM", "KSUM", "VSUM", "VT", "QB", "KB", "P", "OUTC", "SHARP", "SRCSCORE", "SEL",
             "ORDER", "KVMAP", "KC32", "KC", "VCT", "L3", "KN", "VN", "VTN", "NKSUM", "NVSUM"]
 
