@@ -9,47 +9,59 @@
 // n_tgt_tiles + r is source block sel_base + sel[r] (tokens >= Sk are zero keys with
 // logit 0, exactly like the reference's zero padding of k_padded).
 //
-// Workgroup = 4 waves = two 64-row query blocks from the per-head block list (wave w:
-// block w/2, rows 32*(w%2)..+31); two workgroups share a CU so the MFMA work of one wave
-// overlaps the softmax VALU work of another.  K / V^T tiles are double buffered in LDS and
-// arrive by direct global->LDS buffer loads (LDS DMA: lane l of a load lands at M0 + 16 l)
-// issued one tile ahead, so no vector registers stage them; one barrier per tile.  The LDS
-// XOR swizzle is applied on the global side: each lane fetches the chunk that belongs in
-// its LDS slot.  Per-lane global offsets are computed once, the tile start is the scalar
-// base of a buffer resource whose range covers only key rows below Sk, and every LDS
-// offset is hoisted out of the tile loop, so the loop's vector ALU work is the softmax.
+// Workgroup = 8 waves = four 64-row query blocks (wave w: block w/2, rows 32*(w%2)..+31),
+// all sharing each K / V^T tile.  The waves form two groups, G0 = waves 0-3 and G1 = waves
+// 4-7, so every SIMD holds one wave of each.  The groups run the same sequence of phases
+//     GEMM(k) = { S(k) = K(k) Q^T ;  O += V(k-1)^T P(k-1) }      (32 MFMAs)
+//     SOFT(k) = { row max, lazy rescale, P(k) = exp2(S(k) c - m) } (~1000 VALU cycles)
+// G1 one slot behind G0, with a workgroup barrier between slots: in every slot one wave per
+// SIMD feeds the matrix pipe while the other keeps the vector ALU busy ("ping-pong").
 //
-// Lazy rescale: probabilities are taken relative to a reference max m_ref that is raised
-// only when a row max exceeds it by more than FA_RESCALE_LOG2 (so p <= 2^8), so the O / l
-// rescale runs on a few tiles per row.  Exact in real arithmetic.
+// Tiles arrive by direct global->LDS buffer loads (LDS DMA: lane l of a load lands at
+// M0 + 16 l): K(k+1) and V(k) are issued in slot 2k and waited for at the end of slot
+// 2k+1, double buffered.  The LDS XOR swizzle is applied on the global side: each lane
+// fetches the chunk that belongs in its LDS slot.  Per-lane global offsets are computed
+// once, the tile start is the scalar base of a buffer resource whose range covers only key
+// rows below Sk, and every LDS offset is hoisted out of the loop.
+//
+// Softmax state: probabilities are taken relative to a reference max m_ref that is raised
+// only when a row max exceeds it by more than FA_RESCALE_LOG2 (so p <= 2^8); the O / l
+// rescale then runs on a few tiles per row.  Exact in real arithmetic.
 #include "attn_tile.h"
 #include "icsa_kernels.h"
 
-#define FA_QBLK_PER_WG 2
-#define FA_LDS_BYTES (2 * (K_TILE_BYTES + V_TILE_BYTES) + 4096)
+#define FA_WAVES 8
+#define FA_THREADS (FA_WAVES * 64)
+#define FA_QBLK_PER_WG (FA_WAVES / 2)
+#define FA_STAGE_BYTES (FA_WAVES * 32 * O_LDS_STRIDE * 4)    // epilogue staging, all waves
+#define FA_TILE_BYTES (2 * (K_TILE_BYTES + V_TILE_BYTES))
+#define FA_LDS_BYTES (FA_TILE_BYTES > FA_STAGE_BYTES ? FA_TILE_BYTES : FA_STAGE_BYTES)
 #define FA_RESCALE_LOG2 8.0f
+#ifndef FA_PF
+#define FA_PF 3             // operand prefetch depth (MFMA steps)
+#endif
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
   const int n = bytes > 0x7fffffffLL ? 0x7fffffff : (int)bytes;
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, n, 0x00020000);
 }
 
-__device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
-  return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
-}
+typedef __attribute__((address_space(3))) void* lds_ptr;
 
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+__global__ void __launch_bounds__(FA_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
 icsa_flash_kernel(FlashParams p) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-  const int npairs = (p.n_qblk + FA_QBLK_PER_WG - 1) / FA_QBLK_PER_WG;
-  const int work = xcd_remap(blockIdx.x, p.B * p.H * npairs);
+  const int ngrp = (p.n_qblk + FA_QBLK_PER_WG - 1) / FA_QBLK_PER_WG;
+  const int work = xcd_remap(blockIdx.x, p.B * p.H * ngrp);
   if (work < 0) return;
-  const int bh = work / npairs, pair = work % npairs;
+  const int bh = work / ngrp, grp = work % ngrp;
   const int b = bh / p.H, h = bh % p.H;
   const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63;
+  // wave index made provably wave-uniform (a scalar), so per-group branches stay uniform
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int li = lane & 31, hl = lane >> 5;
-  const int slot = pair * FA_QBLK_PER_WG + (wave >> 1);
+  const int group = wave >> 2;                        // 0: leads, 1: one slot behind
+  const int slot = grp * FA_QBLK_PER_WG + (wave >> 1);
   const bool active = slot < p.n_qblk;
   int qblk = 0;
   if (active) qblk = p.qblocks ? p.qblocks[(int64_t)bh * p.qb_stride + p.qb_offset + slot] : slot;
@@ -60,14 +72,14 @@ icsa_flash_kernel(FlashParams p) {
   load_q_frags(qf, p.q + (int64_t)b * p.q_sb + (int64_t)qtok0 * p.q_ss + (int64_t)h * p.q_sh, p.q_ss,
                q_valid);
 
-  // ---- per-lane offsets, hoisted out of the tile loop ----
+  // ---- per-lane offsets, hoisted out of the loop ----
   const bf16* kb = p.k + (int64_t)b * p.k_sb + (int64_t)h * p.k_sh;
   const bf16* vb = p.vt + (int64_t)b * p.vt_sb + (int64_t)h * p.vt_sh;
-  // DMA segment s = 4 * wave + i (1 KB each): K rows 4s..4s+3, V^T rows 8s..8s+7.
-  int kvo[4], vvo[4];
+  // DMA segment s = 2 * wave + i (1 KB each): K rows 4s..4s+3, V^T rows 8s..8s+7.
+  int kvo[2], vvo[2];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int s = 4 * wave + i;
+  for (int i = 0; i < 2; ++i) {
+    const int s = 2 * wave + i;
     const int kr = 4 * s + (lane >> 4), kp = lane & 15;          // LDS row / physical chunk
     const int kc = kp ^ (kr & 15);                               // logical chunk in that slot
     kvo[i] = (int)(((int64_t)kr * p.k_ss + 8 * kc) * 2);
@@ -85,121 +97,174 @@ icsa_flash_kernel(FlashParams p) {
     return j < p.n_tgt_tiles ? j * ATT_BN
                              : (p.sel_base + p.sel[(int64_t)bh * p.sel_stride + (j - p.n_tgt_tiles)]) * ATT_BN;
   };
-  typedef __attribute__((address_space(3))) void* lds_ptr;
-  // Issues the DMA of tile j into LDS buffer buf.  Each tile gets scalar buffer resources
-  // based at its first row; the K range covers key rows below Sk only.  Returns the
-  // number of valid key rows (rows past it are zero-filled by fill_tail after the wait).
-  auto issue_tile = [&](int j, int buf) -> int {
+  auto kbuf = [&](int i) -> unsigned char* { return smem + i * K_TILE_BYTES; };
+  auto vbuf = [&](int i) -> unsigned char* { return smem + 2 * K_TILE_BYTES + i * V_TILE_BYTES; };
+  // DMA of K tile j into K buffer j & 1; the range covers only key rows below Sk.
+  // Returns the number of valid key rows (rows past it are zeroed by fill_tail).
+  auto issue_k = [&](int j) -> int {
     const int tok0 = tile_tok0(j);
     const int k_valid = min(ATT_BN, p.Sk - tok0);
     const int64_t k_bytes = k_valid > 0 ? ((int64_t)(k_valid - 1) * p.k_ss + ICSA_D) * 2 : 0;
     const __amdgpu_buffer_rsrc_t krs = make_rsrc(kb + (int64_t)tok0 * p.k_ss, k_bytes);
-    const __amdgpu_buffer_rsrc_t vrs =
-        make_rsrc(vb + tok0, ((int64_t)(ICSA_D - 1) * p.vt_sd + ATT_BN) * 2);
-    unsigned char* kdst = smem + buf * K_TILE_BYTES + wave * 4096;
-    unsigned char* vdst = smem + 2 * K_TILE_BYTES + buf * V_TILE_BYTES + wave * 4096;
+    unsigned char* dst = kbuf(j & 1) + wave * 2048;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (lds_ptr)(kdst + 1024 * i), 16, kvo[i], 0, 0, 0);
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (lds_ptr)(vdst + 1024 * i), 16, vvo[i], 0, 0, 0);
+    for (int s = 0; s < 2; ++s)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (lds_ptr)(dst + 1024 * s), 16, kvo[s], 0, 0, 0);
     return k_valid;
   };
-  // Zero the key rows >= k_valid of this wave's own DMA segments (rows 16 w .. 16 w + 15)
-  // after its DMA completed, so padding keys are exact zeros.
-  auto fill_tail = [&](int buf, int k_valid) {
-    if (k_valid >= ATT_BN) return;
-    const int row = 16 * wave + (lane >> 2);
-    if (row >= k_valid) {
-      unsigned char* dst = smem + buf * K_TILE_BYTES + row * ICSA_D * 2 + (lane & 3) * 64;
+  auto issue_v = [&](int j) {
+    const int tok0 = tile_tok0(j);
+    const __amdgpu_buffer_rsrc_t vrs =
+        make_rsrc(vb + tok0, ((int64_t)(ICSA_D - 1) * p.vt_sd + ATT_BN) * 2);
+    unsigned char* dst = vbuf(j & 1) + wave * 2048;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4*>(dst + 16 * i) = u32x4{0u, 0u, 0u, 0u};
+    for (int s = 0; s < 2; ++s)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (lds_ptr)(dst + 1024 * s), 16, vvo[s], 0, 0, 0);
+  };
+  // Zero key rows >= k_valid of this wave's own DMA segments (rows 8 w .. 8 w + 7), after
+  // its DMA completed, so padding keys are exact zeros.
+  auto fill_tail = [&](int j, int k_valid) {
+    if (k_valid >= ATT_BN) return;
+    const int row = 8 * wave + (lane >> 3);
+    if (row >= k_valid) {
+      unsigned char* dst = kbuf(j & 1) + row * ICSA_D * 2 + (lane & 7) * 32;
+      *reinterpret_cast<u32x4*>(dst) = u32x4{0u, 0u, 0u, 0u};
+      *reinterpret_cast<u32x4*>(dst + 16) = u32x4{0u, 0u, 0u, 0u};
     }
   };
 
   floatx16 o[4] = {};
+  floatx16 s[2];
+  bf16x8 pf[4];
   float m_ref = -INFINITY, l_run = 0.f;
   const float c = p.scale_log2;
   const int n_tiles = p.n_tgt_tiles + p.n_sel;
 
+  // GEMM(k): O += V(k-1)^T P(k-1) (k >= 1) and S(k) = K(k) Q^T (k < n).  Operands are read
+  // from LDS into registers FA_PF MFMA steps ahead of their use (explicit software
+  // pipeline), so the matrix pipe does not wait on LDS latency.
+  auto gemm = [&](int k) {
+    if (k >= 1) {
+      const unsigned char* vs = vbuf((k - 1) & 1);
+      bf16x8 va[16];
+#pragma unroll
+      for (int t = 0; t < FA_PF; ++t)
+        va[t] = *reinterpret_cast<const bf16x8*>(vs + vro[t >> 2] + (t & 3) * 32 * ATT_BN * 2);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int t = 0; t < 16; ++t) {
+        if (t + FA_PF < 16) {
+          const int u = t + FA_PF;
+          va[u] = *reinterpret_cast<const bf16x8*>(vs + vro[u >> 2] + (u & 3) * 32 * ATT_BN * 2);
+        }
+        o[t & 3] = mfma32x32x16(va[t], pf[t >> 2], o[t & 3]);
+        __builtin_amdgcn_sched_barrier(0);    // keep the read-ahead order
+      }
+    }
+    if (k < n_tiles) {
+      const unsigned char* ks = kbuf(k & 1);
+      bf16x8 ka[16];
+      floatx16 acc0 = {}, acc1 = {};
+#pragma unroll
+      for (int t = 0; t < FA_PF; ++t)
+        ka[t] = *reinterpret_cast<const bf16x8*>(ks + kro[t >> 1] + (t & 1) * 32 * ICSA_D * 2);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int t = 0; t < 16; ++t) {
+        if (t + FA_PF < 16) {
+          const int u = t + FA_PF;
+          ka[u] = *reinterpret_cast<const bf16x8*>(ks + kro[u >> 1] + (u & 1) * 32 * ICSA_D * 2);
+        }
+        if (t & 1) acc1 = mfma32x32x16(ka[t], qf[t >> 1], acc1);
+        else acc0 = mfma32x32x16(ka[t], qf[t >> 1], acc0);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      s[0] = acc0;
+      s[1] = acc1;
+    }
+  };
+  // SOFT(k): mask, row max, lazy rescale, P(k)
+  auto soft = [&](int k) {
+    const int mask_from = k < p.n_tgt_tiles ? p.t_limit - k * ATT_BN : ATT_BN;
+    if (mask_from < ATT_BN) {
+#pragma unroll
+      for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          if (32 * sub + acc_row(i, lane) >= mask_from) s[sub][i] = -INFINITY;
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[sub][i]);
+    mx = xhalf_max(mx) * c;
+    const bool need = mx > m_ref + FA_RESCALE_LOG2;
+    if (__ballot(need) != 0ull) {
+      const float mn = need ? mx : m_ref;
+      const float a = __builtin_amdgcn_exp2f(m_ref - mn);
+#pragma unroll
+      for (int ds = 0; ds < 4; ++ds)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o[ds][i] *= a;
+      l_run *= a;
+      m_ref = mn;
+    }
+    float rs = 0.f;
+#pragma unroll
+    for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const float e = __builtin_amdgcn_exp2f(fmaf(s[sub][i], c, -m_ref));
+        rs += e;
+        pf[2 * sub + (i >> 3)][i & 7] = (bf16)e;
+      }
+    l_run += rs;
+  };
+
+  // Slot schedule.  Slot t ends with a workgroup barrier.  issue(k) = DMA of K(k+1) and
+  // V(k), started at the beginning of slot 2k and waited for at the end of slot 2k+1.
+  // Both groups run the same loop body  [GEMM(k) | barrier | SOFT(k) | barrier]:  group 0
+  // in slots (2k, 2k+1), group 1 one slot later (2k+1, 2k+2) -- it enters with one extra
+  // barrier and group 0 leaves with one, so the barrier counts match.  Only the DMA
+  // issue / wait points differ between the groups.
+  const bool compute = q_valid > 0;
+  const bool lag = group == 1;
+  auto issue = [&](int k) -> int {
+    int kv_next = ATT_BN;
+    if (k + 1 < n_tiles) kv_next = issue_k(k + 1);
+    if (k < n_tiles) issue_v(k);
+    return kv_next;
+  };
+  auto wait_fill = [&](int k, int kv_next) {       // completes issue(k)
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if (k + 1 < n_tiles) fill_tail(k + 1, kv_next);
+  };
+
   {
-    const int kv0 = issue_tile(0, 0);
+    const int kv0 = issue_k(0);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     fill_tail(0, kv0);
   }
   __syncthreads();
-
-  for (int j = 0; j < n_tiles; ++j) {
-    const int buf = j & 1;
-    const bool has_next = j + 1 < n_tiles;
-    int kv_next = ATT_BN;
-    if (has_next) kv_next = issue_tile(j + 1, buf ^ 1);
-    if (q_valid > 0) {
-      const unsigned char* ks = smem + buf * K_TILE_BYTES;
-      const unsigned char* vs = smem + 2 * K_TILE_BYTES + buf * V_TILE_BYTES;
-      floatx16 s[2];
-#pragma unroll
-      for (int sub = 0; sub < 2; ++sub) {
-        floatx16 acc = {};
-#pragma unroll
-        for (int kk = 0; kk < 8; ++kk) {
-          const bf16x8 a = *reinterpret_cast<const bf16x8*>(ks + kro[kk] + sub * 32 * ICSA_D * 2);
-          acc = mfma32x32x16(a, qf[kk], acc);
-        }
-        s[sub] = acc;
-      }
-      const int mask_from = j < p.n_tgt_tiles ? p.t_limit - j * ATT_BN : ATT_BN;
-      if (mask_from < ATT_BN) {
-#pragma unroll
-        for (int sub = 0; sub < 2; ++sub)
-#pragma unroll
-          for (int i = 0; i < 16; ++i)
-            if (32 * sub + acc_row(i, lane) >= mask_from) s[sub][i] = -INFINITY;
-      }
-      float mx = -INFINITY;
-#pragma unroll
-      for (int sub = 0; sub < 2; ++sub)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[sub][i]);
-      mx = xhalf_max(mx) * c;
-      const bool need = mx > m_ref + FA_RESCALE_LOG2;
-      if (__ballot(need) != 0ull) {
-        const float mn = need ? mx : m_ref;
-        const float a = __builtin_amdgcn_exp2f(m_ref - mn);
-#pragma unroll
-        for (int ds = 0; ds < 4; ++ds)
-#pragma unroll
-          for (int i = 0; i < 16; ++i) o[ds][i] *= a;
-        l_run *= a;
-        m_ref = mn;
-      }
-      float rs = 0.f;
-      bf16x8 pf[4];
-#pragma unroll
-      for (int sub = 0; sub < 2; ++sub)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const float e = __builtin_amdgcn_exp2f(fmaf(s[sub][i], c, -m_ref));
-          rs += e;
-          pf[2 * sub + (i >> 3)][i & 7] = (bf16)e;
-        }
-      l_run += rs;
-#pragma unroll
-      for (int m = 0; m < 4; ++m) {
-#pragma unroll
-        for (int ds = 0; ds < 4; ++ds) {
-          const bf16x8 a = *reinterpret_cast<const bf16x8*>(vs + vro[m] + ds * 32 * ATT_BN * 2);
-          o[ds] = mfma32x32x16(a, pf[m], o[ds]);
-        }
-      }
-    }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    if (has_next) fill_tail(buf ^ 1, kv_next);
+  int kv_pending = ATT_BN;
+  if (lag) {                       // slot 0 for group 1: issue(0), then its first barrier
+    kv_pending = issue(0);
     __syncthreads();
   }
+  for (int k = 0; k <= n_tiles; ++k) {
+    if (!lag) kv_pending = issue(k);            // slot 2k starts
+    if (compute) gemm(k);
+    if (lag) wait_fill(k, kv_pending);          // end of slot 2k+1 (group 1 view)
+    __syncthreads();
+    if (lag) kv_pending = issue(k + 1);         // slot 2k+2 starts (group 1 view)
+    if (compute && k < n_tiles) soft(k);
+    if (!lag) wait_fill(k, kv_pending);         // end of slot 2k+1 (group 0 view)
+    __syncthreads();
+  }
+  if (!lag) __syncthreads();       // group 0's extra slot
 
-  // epilogue: stage O through LDS (K/V buffers are free after the last barrier)
+  // ---- epilogue: 1/l, residual, scatter (the workgroup owns the CU's LDS: one round) ----
   float* o_lds = reinterpret_cast<float*>(smem) + wave * 32 * O_LDS_STRIDE;
   const float l_tot = xhalf_sum(l_run);
   const float inv_l = l_tot > 0.f ? 1.f / l_tot : 0.f;
@@ -212,8 +277,8 @@ icsa_flash_kernel(FlashParams p) {
 }
 
 hipError_t launch_flash(const FlashParams& p, hipStream_t stream) {
-  const int npairs = (p.n_qblk + FA_QBLK_PER_WG - 1) / FA_QBLK_PER_WG;
-  const int n_work = p.B * p.H * npairs;
+  const int ngrp = (p.n_qblk + FA_QBLK_PER_WG - 1) / FA_QBLK_PER_WG;
+  const int n_work = p.B * p.H * ngrp;
   if (n_work == 0) return hipSuccess;
   if (p.n_tgt_tiles + p.n_sel <= 0) return hipErrorInvalidValue;
   // per-(b, h) slices must be addressable with 32-bit buffer offsets
@@ -223,6 +288,6 @@ hipError_t launch_flash(const FlashParams& p, hipStream_t stream) {
       reinterpret_cast<const void*>(icsa_flash_kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
       FA_LDS_BYTES);
   if (attr != hipSuccess) return attr;
-  hipLaunchKernelGGL(icsa_flash_kernel, dim3(xcd_grid(n_work)), dim3(256), FA_LDS_BYTES, stream, p);
+  hipLaunchKernelGGL(icsa_flash_kernel, dim3(xcd_grid(n_work)), dim3(FA_THREADS), FA_LDS_BYTES, stream, p);
   return hipGetLastError();
 }
