@@ -433,7 +433,8 @@ SpLayout sparse_layout(int B, int H, int TQ, int TKV, double sparsity) {
 extern "C" {
 
 int64_t icsa_sparse_piecewise_workspace_size(int B, int H, int TQ, int TKV, int D, double sparsity) {
-  if (B <= 0 || H <= 0 || TQ <= 0 || TKV <= 0 || D != ICSA_D) return -1;
+  if (B <= 0 || H <= 0 || TQ <= 0 || TKV <= 0 || D != ICSA_D) return ICSA_EINVAL;
+  if (TQ % ICSA_BLOCK || TKV % ICSA_BLOCK || !(sparsity > 0.0)) return ICSA_EINVAL;
   return sparse_layout(B, H, TQ, TKV, sparsity).total;
 }
 

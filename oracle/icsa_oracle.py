@@ -59,7 +59,7 @@ import torch
 import torch.nn.functional as F
 
 __all__ = [
-    "BLOCK_M", "Sizes", "derive_sizes", "pool_blocks", "compressed_attention",
+    "BLOCK_M", "Sizes", "derive_sizes", "block_sizes", "pool_blocks", "compressed_attention",
     "select_source_blocks", "new_kv_token_map", "gather_new_kv", "split_blocks",
     "sparse_piecewise_attn", "dense_attention", "editing_sparse_attention",
     "ranked_topk", "check_topk_valid", "check_split_valid",

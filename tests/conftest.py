@@ -12,6 +12,7 @@ for p in (ROOT, PKG_PARENT):
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (runs the HIP library on cuda:0)")
+    config.addinivalue_line("markers", "cpu: runs on the host only (oracle, host logic, library load)")
 
 
 @pytest.fixture(scope="session")
