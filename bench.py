@@ -104,6 +104,10 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-dense", action="store_true")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
+                    help="after the timed steps, run 3 elementwise copies (torch.neg) of BYTES "
+                         "bytes: the reference kernel of known traffic that scales the HBM "
+                         "counters of a rocprofv3 --pmc run of this command")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures a single GPU; --gpus {args.gpus} is not supported by this build "
@@ -194,6 +198,16 @@ def main():
         dense = {"ms": dense_ms, "tflops": dense_flops / dense_ms / 1e9,
                  "mfma_frac": dense_flops / dense_ms / 1e9 / PEAK_BF16_TFLOPS}
         log(f"[bench] dense FA {dense_ms:.3f} ms ({dense['tflops']:.1f} TFLOP/s)")
+
+    if args.calibrate_copy:
+        n = args.calibrate_copy // 4
+        src = torch.randn(n, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            torch.neg(src, out=dst)
+        torch.cuda.synchronize()
+        log(f"[bench] calibration copy: 3 x torch.neg over {n * 4} bytes (read {n * 4}, write {n * 4})")
+        del src, dst
 
     fa_ms = stage_ms["flash"]
     fa_tflops = fa_flops / fa_ms / 1e9
