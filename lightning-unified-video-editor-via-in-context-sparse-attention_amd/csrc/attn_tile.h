@@ -22,6 +22,15 @@
 #define K_TILE_BYTES (ATT_BN * ICSA_D * 2)    // 16 KB
 #define V_TILE_BYTES (ICSA_D * ATT_BN * 2)    // 16 KB
 
+// Raw buffer resource over [base, base + bytes): loads past the range return no data,
+// which keeps a tile's DMA inside the rows that exist.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
+  const int n = bytes > 0x7fffffffLL ? 0x7fffffff : (int)(bytes < 0 ? 0 : bytes);
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, n, 0x00020000);
+}
+
+typedef __attribute__((address_space(3))) void* lds_ptr;
+
 // Register staging of one K + V^T tile for a workgroup of NT threads (NT = 256 or 128).
 template <int NT>
 struct TileRegs {

@@ -41,13 +41,6 @@
 #define FA_PF 3             // operand prefetch depth (MFMA steps)
 #endif
 
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
-  const int n = bytes > 0x7fffffffLL ? 0x7fffffff : (int)bytes;
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, n, 0x00020000);
-}
-
-typedef __attribute__((address_space(3))) void* lds_ptr;
-
 __global__ void __launch_bounds__(FA_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
 icsa_flash_kernel(FlashParams p) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];

@@ -12,125 +12,242 @@
 //      are never rescaled afterwards -- the reference's behaviour, kept on purpose;
 //   3. out = (acc + g_acc) / (l + g_l), 0 when the denominator is 0 (:980-992).
 //
+// Equivalent schedule used here.  The rescales of acc / l during the interval compose to
+// one factor exp2(m_exact - m_final), so the interval runs twice over the compressed
+// chunks: pass 1 computes only the running max (-> m_final), acc / l are rescaled once,
+// and pass 2 recomputes the same running max chunk by chunk and accumulates the
+// non-rescaled g terms straight into the output accumulator.  That costs one extra
+// Q.KC product per chunk and frees the separate g accumulator (64 registers), which is
+// what lets two waves share each SIMD.
+//
 // The new KV is read in place: new-KV block j lives at source block kvmap[j] of the
 // (k, vt) buffers -- target blocks and the selected source blocks of the original
-// sequence -- or is an all-zero block (kvmap -1, the reference's TKV zero padding, which
-// is attended with logit 0).  KC / VC^T are the bf16 block sums of the new KV.
+// sequence -- or is an all-zero block (kvmap -1 / an out-of-range caller index, the
+// reference's TKV zero padding, attended with logit 0).  KC / VC^T are the bf16 block sums
+// of the new KV.
 //
-// Workgroup = 2 waves = one query block (wave w: rows 32*w..+31).  Epilogue fuses the
-// residual and the scatter to [B, S, H, D] like the flash-attention kernel.
+// Workgroup = 2 waves = one query block (wave w: rows 32 w .. 32 w + 31); four workgroups
+// share a CU.  One K buffer and one V^T buffer per workgroup, filled by direct
+// global->LDS loads (lane l lands at M0 + 16 l; the XOR swizzle is applied on the global
+// side).  K(t+1) is issued as soon as both waves finished reading K(t) and lands while
+// the softmax and PV of tile t run; V(t+1) is issued after PV(t) and lands during QK and
+// softmax of tile t+1.  The epilogue fuses the residual and the scatter to [B, S, H, D].
 #include "attn_tile.h"
 #include "icsa_kernels.h"
 
 #define SP_THREADS 128
 #define SP_MAX_TOPK 512
-// K tile + V^T tile (32 KB), or the epilogue's 2 x 32 x O_LDS_STRIDE fp32 staging rows
-#define SP_LDS_BYTES (2 * 32 * O_LDS_STRIDE * 4 > K_TILE_BYTES + V_TILE_BYTES \
-                          ? 2 * 32 * O_LDS_STRIDE * 4 : K_TILE_BYTES + V_TILE_BYTES)
+#define SP_MAX_CHUNKS 32                 // NKV <= 2048
+// one wave's fp32 output staging rows; each tile buffer is at least that large
+#define SP_STAGE_BYTES (32 * O_LDS_STRIDE * 4)
+#define SP_BUF_BYTES (SP_STAGE_BYTES > K_TILE_BYTES ? SP_STAGE_BYTES : K_TILE_BYTES)
+#define SP_RESCALE_LOG2 8.0f
+#define SP_PF 3                          // MFMA operand read-ahead (steps)
+#define SP_DMA_PER_TILE 8                // LDS-DMA instructions per wave per K or V^T tile
 
-__global__ void __launch_bounds__(SP_THREADS) icsa_sparse_kernel(SparseParams p) {
-  // K tile | V^T tile, reused as the fp32 output staging area in the epilogue
-  __shared__ __attribute__((aligned(16))) unsigned char smem[SP_LDS_BYTES];
-  __shared__ int idx_l[SP_MAX_TOPK];
-  bf16* ks = reinterpret_cast<bf16*>(smem);
-  bf16* vs = reinterpret_cast<bf16*>(smem + K_TILE_BYTES);
+// vmcnt waits: "all but the newest tile" / "everything".  Loads complete in issue order.
+#define SP_WAIT_OLDER() asm volatile("s_waitcnt vmcnt(8)" ::: "memory")
+#define SP_WAIT_ALL() asm volatile("s_waitcnt vmcnt(0)" ::: "memory")
+// Workgroup barrier without a memory fence: __syncthreads() would also wait for every
+// outstanding LDS-DMA load (vmcnt(0)), which defeats the prefetch.  LDS reads and writes
+// issued before it are complete (lgkmcnt(0)); tile DMA is waited for explicitly above.
+#define SP_BARRIER() asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory")
+
+__global__ void __launch_bounds__(SP_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
+icsa_sparse_kernel(SparseParams p) {
+  // K tile and V^T tile as separate objects, so the compiler can tell a load into one from
+  // reads of the other; in the epilogue they hold the fp32 output rows of wave 0 / wave 1.
+  __shared__ __attribute__((aligned(16))) unsigned char kbuf[SP_BUF_BYTES];
+  __shared__ __attribute__((aligned(16))) unsigned char vbuf[SP_BUF_BYTES];
+  __shared__ int src_l[SP_MAX_TOPK];                  // source block of exact tile t (-1: zeros)
+  __shared__ unsigned long long sel_l[SP_MAX_CHUNKS];  // selected new-KV blocks per chunk
 
   const int n_work = p.B * p.H * p.n_qblk;
   const int work = xcd_remap(blockIdx.x, n_work);
   if (work < 0) return;
   const int bh = work / p.n_qblk, slot = work % p.n_qblk;
   const int b = bh / p.H, h = bh % p.H;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int li = lane & 31, hl = lane >> 5;
   const int qblk = p.qblocks ? p.qblocks[(int64_t)bh * p.qb_stride + p.qb_offset + slot] : slot;
   const int qtok0 = qblk * ICSA_BLOCK + 32 * wave;
   const int q_valid = max(0, min(32, p.Sq - qtok0));
 
   const int top_k = p.top_k;
-  const int* idx_g = p.idx + ((int64_t)bh * p.n_qblk + slot) * top_k;
-  for (int t = threadIdx.x; t < top_k; t += SP_THREADS) idx_l[t] = idx_g[t];
+  const int nc = (p.NKV + ATT_BN - 1) / ATT_BN;      // interval chunks
+  const int T1 = top_k, T2 = top_k + nc, T = top_k + 2 * nc;
+
+  // ---- block lists: source blocks of the exact tiles, selection bitmask per chunk ----
+  for (int c = tid; c < nc; c += SP_THREADS) sel_l[c] = 0ull;
+  __syncthreads();
+  {
+    const int* idx_g = p.idx + ((int64_t)bh * p.n_qblk + slot) * top_k;
+    const int* kvmap = p.kvmap + (int64_t)bh * p.NKV;
+    for (int t = tid; t < top_k; t += SP_THREADS) {
+      const int j = idx_g[t];
+      int src = -1;                 // out-of-range entries of a caller list: a zero block
+      if (j >= 0 && j < p.NKV) {
+        src = p.kvmap_identity ? j : kvmap[j];
+        atomicOr(&sel_l[j >> 6], 1ull << (j & 63));
+      }
+      src_l[t] = src;
+    }
+  }
 
   bf16x8 qf[8];
   load_q_frags(qf, p.q + (int64_t)b * p.q_sb + (int64_t)qtok0 * p.q_ss + (int64_t)h * p.q_sh, p.q_ss,
                q_valid);
-  __syncthreads();
 
-  floatx16 o[4] = {};
-  float m_run = -INFINITY, l_run = 0.f;
-  const float c = p.scale_log2;
-  const int* kvmap = p.kvmap + (int64_t)bh * p.NKV;
+  // ---- DMA segments ----
+  // K tile: this wave's rows 32 w .. 32 w + 31 in 8 one-KB segments of 4 rows (segment i:
+  // rows 32 w + 4 i + lane / 16, lane % 16 = physical 16-byte chunk).
+  // V^T tile: d rows 64 w .. 64 w + 63 in 8 segments of 8 rows (d = 64 w + 8 i + lane / 8).
   const bf16* kbase = p.k + (int64_t)b * p.k_sb + (int64_t)h * p.k_sh;
   const bf16* vtbase = p.vt + (int64_t)b * p.vt_sb + (int64_t)h * p.vt_sh;
-  TileRegs<SP_THREADS> regs;
-
-  // ---- 1. exact blocks ----
-  for (int t = 0; t < top_k; ++t) {
-    const int j = idx_l[t];
-    // out-of-range entries of a caller-provided list read as an all-zero block
-    const int src = (j < 0 || j >= p.NKV) ? -1 : (p.kvmap_identity ? j : kvmap[j]);
-    if (src >= 0) {
-      const int tok0 = src * ATT_BN;
-      tile_load_regs(regs, kbase + (int64_t)tok0 * p.k_st, p.k_st, min(ATT_BN, p.Sk - tok0),
-                     vtbase + tok0, p.vt_sd, false);
-    } else {
-      tile_load_regs(regs, kbase, p.k_st, 0, vtbase, p.vt_sd, true);
-    }
-    if (t > 0) __syncthreads();                 // previous tile fully consumed
-    tile_store_lds(regs, ks, vs);
-    __syncthreads();
-    floatx16 s[2];
-    qk_tile(s, ks, qf);
-    float mx = -INFINITY;
-#pragma unroll
-    for (int sub = 0; sub < 2; ++sub)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[sub][i]);
-    mx = xhalf_max(mx);
-    const float m_new = fmaxf(m_run, mx * c);
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-    float rs = 0.f;
-#pragma unroll
-    for (int sub = 0; sub < 2; ++sub)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const float e = __builtin_amdgcn_exp2f(fmaf(s[sub][i], c, -m_new));
-        s[sub][i] = e;
-        rs += e;
-      }
-    l_run = fmaf(l_run, alpha, rs);
-    if (__ballot(m_new != m_run) != 0ull) {
-#pragma unroll
-      for (int ds = 0; ds < 4; ++ds)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) o[ds][i] *= alpha;
-    }
-    m_run = m_new;
-    bf16x8 pf[4];
-    pack_p(pf, s);
-    pv_tile(o, vs, pf);
-  }
-
-  // ---- 2. interval approximation over chunks of 64 compressed blocks ----
-  floatx16 g[4] = {};
-  float gl_run = 0.f;
-  const float c64 = c * (1.0f / 64.0f);
   const bf16* kcb = p.kc + (int64_t)bh * p.NKVp * ICSA_D;
   const bf16* vcb = p.vct + (int64_t)bh * ICSA_D * p.NKVp;
-  const int n_chunks = (p.NKV + ATT_BN - 1) / ATT_BN;
-  int tptr = 0;                                    // first idx_l entry >= chunk start
-  for (int ch = 0; ch < n_chunks; ++ch) {
-    const int j0 = ch * ATT_BN;
-    tile_load_regs(regs, kcb + (int64_t)j0 * ICSA_D, ICSA_D, ATT_BN, vcb + j0, p.NKVp, false);
-    // selection mask of this chunk (idx_l ascending)
-    unsigned long long selm = 0ull;
-    while (tptr < top_k && idx_l[tptr] < j0 + ATT_BN) {
-      if (idx_l[tptr] >= j0) selm |= 1ull << (idx_l[tptr] - j0);
-      ++tptr;
+  const int k_row0 = 32 * wave + (lane >> 4);        // key row of K segment 0
+  const int v_row0 = 64 * wave + (lane >> 3);        // d row of V^T segment 0
+  int kro[8], vro[4];                                 // MFMA operand read offsets (bytes)
+#pragma unroll
+  for (int kk = 0; kk < 8; ++kk) kro[kk] = k_lds_off(li, 2 * kk + hl) * 2;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) vro[m] = v_lds_off(li, 2 * m + hl) * 2;
+
+  __syncthreads();                                    // src_l / sel_l ready
+
+  // Tile g: g < T1 exact block src_l[g]; T1 <= g < T2 pass-1 chunk g - T1 (K only);
+  // g >= T2 pass-2 chunk g - T2.  issue_k returns the number of real key rows (the rest
+  // are zeroed after the wait); issue_v returns whether the V^T tile is all zeros.
+  auto issue_k = [&](int g) -> int {
+    const bf16* base;
+    int64_t bytes;
+    int valid, rs2;                        // rs2: key row stride in bytes
+    const bool ex = g < T1;
+    if (ex) {
+      const int src = __builtin_amdgcn_readfirstlane(src_l[g]);
+      const int tok0 = src * ATT_BN;
+      valid = src < 0 ? 0 : min(ATT_BN, p.Sk - tok0);
+      base = kbase + (src < 0 ? 0 : (int64_t)tok0 * p.k_st);
+      bytes = valid > 0 ? ((int64_t)(valid - 1) * p.k_st + ICSA_D) * 2 : 0;
+      rs2 = (int)p.k_st * 2;
+    } else {
+      const int c = g < T2 ? g - T1 : g - T2;
+      valid = ATT_BN;
+      base = kcb + (int64_t)c * ATT_BN * ICSA_D;
+      bytes = (int64_t)ATT_BN * ICSA_D * 2;
+      rs2 = ICSA_D * 2;
     }
-    __syncthreads();
-    tile_store_lds(regs, ks, vs);
-    __syncthreads();
-    floatx16 s[2];
-    qk_tile(s, ks, qf);
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(base, bytes);
+    unsigned char* dst = kbuf + wave * 8192;
+#pragma unroll
+    for (int i = 0; i < SP_DMA_PER_TILE; ++i) {
+      const int r = k_row0 + 4 * i;
+      const int off = r * rs2 + (((lane & 15) ^ (r & 15)) << 4);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)(dst + 1024 * i), 16, off, 0, 0, 0);
+    }
+    return valid;
+  };
+  auto issue_v = [&](int g) -> bool {
+    const bf16* base;
+    int64_t bytes;
+    bool zero = false;
+    int rs2;                               // V^T row stride in bytes
+    const bool ex = g < T1;
+    if (ex) {
+      const int src = __builtin_amdgcn_readfirstlane(src_l[g]);
+      zero = src < 0;
+      base = vtbase + (zero ? 0 : (int64_t)src * ATT_BN);
+      bytes = zero ? 0 : ((int64_t)(ICSA_D - 1) * p.vt_sd + ATT_BN) * 2;
+      rs2 = (int)p.vt_sd * 2;
+    } else {
+      const int c = g - T2;
+      base = vcb + (int64_t)c * ATT_BN;
+      bytes = ((int64_t)(ICSA_D - 1) * p.NKVp + ATT_BN) * 2;
+      rs2 = p.NKVp * 2;
+    }
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(base, bytes);
+    unsigned char* dst = vbuf + wave * 8192;
+#pragma unroll
+    for (int i = 0; i < SP_DMA_PER_TILE; ++i) {
+      const int d = v_row0 + 8 * i;
+      const int off = d * rs2 + (((lane & 7) ^ ((d >> 1) & 7)) << 4);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)(dst + 1024 * i), 16, off, 0, 0, 0);
+    }
+    return zero;
+  };
+  // After the wait: zero this wave's K rows >= valid / its whole V^T half (zero blocks).
+  auto fill_k = [&](int valid) {
+    if (valid >= ATT_BN) return;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int r = 32 * wave + 4 * i + (lane >> 4);
+      if (r >= valid) *reinterpret_cast<u32x4*>(kbuf + r * ICSA_D * 2 + (lane & 15) * 16) = u32x4{0u, 0u, 0u, 0u};
+    }
+  };
+  auto fill_v = [&](bool zero) {
+    if (!zero) return;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int d = 64 * wave + 8 * i + (lane >> 3);
+      *reinterpret_cast<u32x4*>(vbuf + d * ATT_BN * 2 + (lane & 7) * 16) = u32x4{0u, 0u, 0u, 0u};
+    }
+  };
+
+  floatx16 o[4] = {};
+  floatx16 s[2];
+  bf16x8 pf[4];
+
+  // S^T = K Q^T for the K buffer; operands read SP_PF steps ahead of their MFMA.
+  auto qk = [&]() {
+    bf16x8 ka[16];
+    floatx16 acc0 = {}, acc1 = {};
+#pragma unroll
+    for (int t = 0; t < SP_PF; ++t)
+      ka[t] = *reinterpret_cast<const bf16x8*>(kbuf + kro[t >> 1] + (t & 1) * 32 * ICSA_D * 2);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int t = 0; t < 16; ++t) {
+      if (t + SP_PF < 16) {
+        const int u = t + SP_PF;
+        ka[u] = *reinterpret_cast<const bf16x8*>(kbuf + kro[u >> 1] + (u & 1) * 32 * ICSA_D * 2);
+      }
+      if (t & 1) acc1 = mfma32x32x16(ka[t], qf[t >> 1], acc1);
+      else acc0 = mfma32x32x16(ka[t], qf[t >> 1], acc0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    s[0] = acc0;
+    s[1] = acc1;
+  };
+  // O^T += V^T P^T for the V^T buffer
+  auto pv = [&]() {
+    bf16x8 va[16];
+#pragma unroll
+    for (int t = 0; t < SP_PF; ++t)
+      va[t] = *reinterpret_cast<const bf16x8*>(vbuf + vro[t >> 2] + (t & 3) * 32 * ATT_BN * 2);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int t = 0; t < 16; ++t) {
+      if (t + SP_PF < 16) {
+        const int u = t + SP_PF;
+        va[u] = *reinterpret_cast<const bf16x8*>(vbuf + vro[u >> 2] + (u & 3) * 32 * ATT_BN * 2);
+      }
+      o[t & 3] = mfma32x32x16(va[t], pf[t >> 2], o[t & 3]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  auto rescale_o = [&](float a) {
+#pragma unroll
+    for (int ds = 0; ds < 4; ++ds)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) o[ds][i] *= a;
+  };
+  // interval scores of one chunk: z = s c / 64, -inf for selected blocks and blocks >= NKV
+  auto interval_z = [&](int c) -> float {
+    const unsigned long long selm = sel_l[c];
+    const int j0 = c * ATT_BN;
+    const float c64 = p.scale_log2 * (1.0f / 64.0f);
     float mx = -INFINITY;
 #pragma unroll
     for (int sub = 0; sub < 2; ++sub)
@@ -142,41 +259,111 @@ __global__ void __launch_bounds__(SP_THREADS) icsa_sparse_kernel(SparseParams p)
         s[sub][i] = z;
         mx = fmaxf(mx, z);
       }
-    mx = xhalf_max(mx);
-    const float m_new = fmaxf(m_run, mx);
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-    l_run *= alpha;
-    if (__ballot(m_new != m_run) != 0ull) {
+    return xhalf_max(mx);
+  };
+
+  const float c = p.scale_log2;
+  float m_ref = -INFINITY;      // reference max of the exact part (raised lazily)
+  float m_true = -INFINITY;     // exact running max (the reference's m after the exact loop)
+  float l_run = 0.f;
+
+  int kv_pending = issue_k(0);
+  bool vz_pending = issue_v(0);
+
+  // ---- 1. exact blocks ----
+  for (int t = 0; t < T1; ++t) {
+    SP_WAIT_OLDER();                       // K(t); V(t) is the newer tile in flight
+    fill_k(kv_pending);
+    SP_BARRIER();
+    qk();
+    SP_BARRIER();                       // K buffer free
+    const int kv_next = issue_k(t + 1);    // T > T1: always a next K tile
+    float mx = -INFINITY;
 #pragma unroll
-      for (int ds = 0; ds < 4; ++ds)
+    for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) o[ds][i] *= alpha;
+      for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[sub][i]);
+    mx = xhalf_max(mx) * c;
+    m_true = fmaxf(m_true, mx);
+    const bool need = mx > m_ref + SP_RESCALE_LOG2;
+    if (__ballot(need) != 0ull) {
+      const float mn = need ? mx : m_ref;
+      const float a = __builtin_amdgcn_exp2f(m_ref - mn);
+      rescale_o(a);
+      l_run *= a;
+      m_ref = mn;
     }
-    m_run = m_new;
     float rs = 0.f;
 #pragma unroll
     for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const float e = __builtin_amdgcn_exp2f(s[sub][i] - m_new);
-        s[sub][i] = e;
+        const float e = __builtin_amdgcn_exp2f(fmaf(s[sub][i], c, -m_ref));
         rs += e;
+        pf[2 * sub + (i >> 3)][i & 7] = (bf16)e;
+      }
+    l_run += rs;
+    SP_WAIT_OLDER();                       // V(t); K(t+1) is the newer tile in flight
+    fill_v(vz_pending);
+    SP_BARRIER();
+    pv();
+    SP_BARRIER();                       // V buffer free
+    vz_pending = issue_v(t + 1 < T1 ? t + 1 : T2);
+    kv_pending = kv_next;
+  }
+
+  // ---- 2a. interval pass 1: running max over the chunks ----
+  float m_run = m_true;
+  for (int ch = 0; ch < nc; ++ch) {
+    if (ch == 0) SP_WAIT_OLDER();          // V(T2) was issued after K(T1)
+    else SP_WAIT_ALL();
+    SP_BARRIER();
+    qk();
+    SP_BARRIER();
+    issue_k(T1 + ch + 1);                  // the last one is pass 2's first K tile
+    m_run = fmaxf(m_run, interval_z(ch));
+  }
+  // acc / l as the reference holds them after every interval rescale
+  {
+    const float a = __builtin_amdgcn_exp2f(m_ref - m_run);
+    rescale_o(a);
+    l_run *= a;
+  }
+
+  // ---- 2b. interval pass 2: non-rescaled g terms, accumulated into o ----
+  float m_c = m_true, gl_run = 0.f;
+  for (int ch = 0; ch < nc; ++ch) {
+    const int g = T2 + ch;
+    if (ch == 0) SP_WAIT_ALL();            // K(T2) is the newest load
+    else SP_WAIT_OLDER();                  // V(g) is newer than K(g)
+    SP_BARRIER();
+    qk();
+    SP_BARRIER();
+    const bool more = g + 1 < T;
+    if (more) issue_k(g + 1);
+    m_c = fmaxf(m_c, interval_z(ch));
+    float rs = 0.f;
+#pragma unroll
+    for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const float e = __builtin_amdgcn_exp2f(s[sub][i] - m_c);
+        rs += e;
+        pf[2 * sub + (i >> 3)][i & 7] = (bf16)e;
       }
     gl_run += rs;
-    bf16x8 pf[4];
-    pack_p(pf, s);
-    pv_tile(g, vs, pf);
+    if (more) SP_WAIT_OLDER();
+    else SP_WAIT_ALL();
+    SP_BARRIER();
+    pv();
+    SP_BARRIER();
+    if (more) issue_v(g + 1);
   }
 
   // ---- 3. combine + epilogue ----
   const float den = xhalf_sum(l_run) + 64.0f * xhalf_sum(gl_run);
   const float inv = den == 0.f ? 0.f : 1.f / den;
-#pragma unroll
-  for (int ds = 0; ds < 4; ++ds)
-#pragma unroll
-    for (int i = 0; i < 16; ++i) o[ds][i] += g[ds][i];
-  __syncthreads();
-  float* o_lds = reinterpret_cast<float*>(smem) + wave * 32 * O_LDS_STRIDE;
+  float* o_lds = reinterpret_cast<float*>(wave == 0 ? kbuf : vbuf);
   stage_o(o_lds, o, inv);
   __syncthreads();
   if (q_valid > 0) {
@@ -189,7 +376,12 @@ hipError_t launch_sparse(const SparseParams& p, hipStream_t stream) {
   const int n_work = p.B * p.H * p.n_qblk;
   if (n_work == 0) return hipSuccess;
   if (p.top_k < 1 || p.top_k > SP_MAX_TOPK || p.top_k > p.NKV) return hipErrorInvalidValue;
+  if (p.NKV < 1 || p.NKV > SP_MAX_CHUNKS * ATT_BN) return hipErrorInvalidValue;
   if (p.NKVp % ATT_BN != 0 || p.NKVp < p.NKV) return hipErrorInvalidValue;
+  // per-(b, h) slices must be addressable with 32-bit buffer offsets
+  if ((int64_t)p.Sk * p.k_st * 2 > 0x7fffffffLL || (int64_t)ICSA_D * p.vt_sd * 2 > 0x7fffffffLL ||
+      16LL * p.k_st * 2 > 0x7fffffffLL)
+    return hipErrorInvalidValue;
   hipLaunchKernelGGL(icsa_sparse_kernel, dim3(xcd_grid(n_work)), dim3(SP_THREADS), 0, stream, p);
   return hipGetLastError();
 }
