@@ -31,6 +31,12 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, in
 
 typedef __attribute__((address_space(3))) void* lds_ptr;
 
+// Workgroup barrier without a memory fence.  __syncthreads() also waits for every
+// outstanding LDS-DMA load (vmcnt(0)), which would cut a tile prefetch short; kernels
+// using this wait for their tile DMA explicitly.  LDS reads and writes issued before the
+// barrier are complete when it is passed (lgkmcnt(0)).
+#define ATT_BARRIER() asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory")
+
 // Register staging of one K + V^T tile for a workgroup of NT threads (NT = 256 or 128).
 template <int NT>
 struct TileRegs {

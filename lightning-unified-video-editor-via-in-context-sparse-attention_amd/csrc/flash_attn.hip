@@ -35,7 +35,9 @@
 #define FA_QBLK_PER_WG (FA_WAVES / 2)
 #define FA_STAGE_BYTES (FA_WAVES * 32 * O_LDS_STRIDE * 4)    // epilogue staging, all waves
 #define FA_TILE_BYTES (2 * (K_TILE_BYTES + V_TILE_BYTES))
-#define FA_LDS_BYTES (FA_TILE_BYTES > FA_STAGE_BYTES ? FA_TILE_BYTES : FA_STAGE_BYTES)
+#define FA_MAX_SEL 4096                                      // extra tiles (LDS list)
+#define FA_LDS_BYTES (FA_TILE_BYTES + 4 * FA_MAX_SEL > FA_STAGE_BYTES ? FA_TILE_BYTES + 4 * FA_MAX_SEL \
+                                                                    : FA_STAGE_BYTES)
 #define FA_RESCALE_LOG2 8.0f
 #ifndef FA_PF
 #define FA_PF 3             // operand prefetch depth (MFMA steps)
@@ -61,9 +63,15 @@ icsa_flash_kernel(FlashParams p) {
   const int qtok0 = qblk * ICSA_BLOCK + 32 * (wave & 1);
   const int q_valid = active ? max(0, min(32, p.Sq - qtok0)) : 0;
 
+  // token start of every extra (selected source) tile, kept in LDS past the tile buffers
+  int* sel_l = reinterpret_cast<int*>(smem + FA_TILE_BYTES);
+  for (int r = tid; r < p.n_sel; r += FA_THREADS)
+    sel_l[r] = (p.sel_base + p.sel[(int64_t)bh * p.sel_stride + r]) * ATT_BN;
+
   bf16x8 qf[8];
   load_q_frags(qf, p.q + (int64_t)b * p.q_sb + (int64_t)qtok0 * p.q_ss + (int64_t)h * p.q_sh, p.q_ss,
                q_valid);
+  __syncthreads();                                    // sel_l ready
 
   // ---- per-lane offsets, hoisted out of the loop ----
   const bf16* kb = p.k + (int64_t)b * p.k_sb + (int64_t)h * p.k_sh;
@@ -87,8 +95,7 @@ icsa_flash_kernel(FlashParams p) {
   for (int m = 0; m < 4; ++m) vro[m] = v_lds_off(li, 2 * m + hl) * 2;        // + 32 d rows per sub-tile
 
   auto tile_tok0 = [&](int j) -> int {
-    return j < p.n_tgt_tiles ? j * ATT_BN
-                             : (p.sel_base + p.sel[(int64_t)bh * p.sel_stride + (j - p.n_tgt_tiles)]) * ATT_BN;
+    return j < p.n_tgt_tiles ? j * ATT_BN : __builtin_amdgcn_readfirstlane(sel_l[j - p.n_tgt_tiles]);
   };
   auto kbuf = [&](int i) -> unsigned char* { return smem + i * K_TILE_BYTES; };
   auto vbuf = [&](int i) -> unsigned char* { return smem + 2 * K_TILE_BYTES + i * V_TILE_BYTES; };
@@ -243,19 +250,19 @@ icsa_flash_kernel(FlashParams p) {
   int kv_pending = ATT_BN;
   if (lag) {                       // slot 0 for group 1: issue(0), then its first barrier
     kv_pending = issue(0);
-    __syncthreads();
+    ATT_BARRIER();
   }
   for (int k = 0; k <= n_tiles; ++k) {
     if (!lag) kv_pending = issue(k);            // slot 2k starts
     if (compute) gemm(k);
     if (lag) wait_fill(k, kv_pending);          // end of slot 2k+1 (group 1 view)
-    __syncthreads();
+    ATT_BARRIER();
     if (lag) kv_pending = issue(k + 1);         // slot 2k+2 starts (group 1 view)
     if (compute && k < n_tiles) soft(k);
     if (!lag) wait_fill(k, kv_pending);         // end of slot 2k+1 (group 0 view)
-    __syncthreads();
+    ATT_BARRIER();
   }
-  if (!lag) __syncthreads();       // group 0's extra slot
+  if (!lag) ATT_BARRIER();       // group 0's extra slot
 
   // ---- epilogue: 1/l, residual, scatter (the workgroup owns the CU's LDS: one round) ----
   float* o_lds = reinterpret_cast<float*>(smem) + wave * 32 * O_LDS_STRIDE;
@@ -273,7 +280,7 @@ hipError_t launch_flash(const FlashParams& p, hipStream_t stream) {
   const int ngrp = (p.n_qblk + FA_QBLK_PER_WG - 1) / FA_QBLK_PER_WG;
   const int n_work = p.B * p.H * ngrp;
   if (n_work == 0) return hipSuccess;
-  if (p.n_tgt_tiles + p.n_sel <= 0) return hipErrorInvalidValue;
+  if (p.n_tgt_tiles + p.n_sel <= 0 || p.n_sel > FA_MAX_SEL) return hipErrorInvalidValue;
   // per-(b, h) slices must be addressable with 32-bit buffer offsets
   if ((int64_t)p.Sk * p.k_ss * 2 > 0x7fffffffLL || (int64_t)ICSA_D * p.vt_sd * 2 > 0x7fffffffLL)
     return hipErrorInvalidValue;

@@ -48,10 +48,6 @@
 // vmcnt waits: "all but the newest tile" / "everything".  Loads complete in issue order.
 #define SP_WAIT_OLDER() asm volatile("s_waitcnt vmcnt(8)" ::: "memory")
 #define SP_WAIT_ALL() asm volatile("s_waitcnt vmcnt(0)" ::: "memory")
-// Workgroup barrier without a memory fence: __syncthreads() would also wait for every
-// outstanding LDS-DMA load (vmcnt(0)), which defeats the prefetch.  LDS reads and writes
-// issued before it are complete (lgkmcnt(0)); tile DMA is waited for explicitly above.
-#define SP_BARRIER() asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory")
 
 __global__ void __launch_bounds__(SP_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
 icsa_sparse_kernel(SparseParams p) {
@@ -274,9 +270,9 @@ icsa_sparse_kernel(SparseParams p) {
   for (int t = 0; t < T1; ++t) {
     SP_WAIT_OLDER();                       // K(t); V(t) is the newer tile in flight
     fill_k(kv_pending);
-    SP_BARRIER();
+    ATT_BARRIER();
     qk();
-    SP_BARRIER();                       // K buffer free
+    ATT_BARRIER();                       // K buffer free
     const int kv_next = issue_k(t + 1);    // T > T1: always a next K tile
     float mx = -INFINITY;
 #pragma unroll
@@ -305,9 +301,9 @@ icsa_sparse_kernel(SparseParams p) {
     l_run += rs;
     SP_WAIT_OLDER();                       // V(t); K(t+1) is the newer tile in flight
     fill_v(vz_pending);
-    SP_BARRIER();
+    ATT_BARRIER();
     pv();
-    SP_BARRIER();                       // V buffer free
+    ATT_BARRIER();                       // V buffer free
     vz_pending = issue_v(t + 1 < T1 ? t + 1 : T2);
     kv_pending = kv_next;
   }
@@ -317,9 +313,9 @@ icsa_sparse_kernel(SparseParams p) {
   for (int ch = 0; ch < nc; ++ch) {
     if (ch == 0) SP_WAIT_OLDER();          // V(T2) was issued after K(T1)
     else SP_WAIT_ALL();
-    SP_BARRIER();
+    ATT_BARRIER();
     qk();
-    SP_BARRIER();
+    ATT_BARRIER();
     issue_k(T1 + ch + 1);                  // the last one is pass 2's first K tile
     m_run = fmaxf(m_run, interval_z(ch));
   }
@@ -336,9 +332,9 @@ icsa_sparse_kernel(SparseParams p) {
     const int g = T2 + ch;
     if (ch == 0) SP_WAIT_ALL();            // K(T2) is the newest load
     else SP_WAIT_OLDER();                  // V(g) is newer than K(g)
-    SP_BARRIER();
+    ATT_BARRIER();
     qk();
-    SP_BARRIER();
+    ATT_BARRIER();
     const bool more = g + 1 < T;
     if (more) issue_k(g + 1);
     m_c = fmaxf(m_c, interval_z(ch));
@@ -354,9 +350,9 @@ icsa_sparse_kernel(SparseParams p) {
     gl_run += rs;
     if (more) SP_WAIT_OLDER();
     else SP_WAIT_ALL();
-    SP_BARRIER();
+    ATT_BARRIER();
     pv();
-    SP_BARRIER();
+    ATT_BARRIER();
     if (more) issue_v(g + 1);
   }
 
