@@ -108,6 +108,9 @@ Layout editing_layout(int B, int S, int H, const Sizes& z, int t, int q_dtype, i
   sz[ICSA_WS_VTN] = unaligned ? BH * D * Tp * 2 : 0;
   sz[ICSA_WS_NKSUM] = unaligned ? BH * z.NKV * D * 4 : 0;
   sz[ICSA_WS_NVSUM] = unaligned ? BH * z.NKV * D * 4 : 0;
+  sz[ICSA_WS_COLP] = BH * ceil_div(z.n_t, ICSA_BLOCK) * std::max(z.n_s, 1) * 4;
+  sz[ICSA_WS_L3S] = BH * std::max(z.n_diffuse, 1) * z.NKV * 4;
+  sz[ICSA_WS_RSTAT] = BH * z.NB * 2 * 4;
   Layout L;
   int64_t o = 0;
   for (int i = 0; i < ICSA_WS_COUNT; ++i) {
@@ -265,7 +268,9 @@ int editing_impl(ICSA_EDITING_ARGS, void* const* stage_events) {
   cp.P = reinterpret_cast<float*>(WS(ICSA_WS_P));
   cp.out_c = reinterpret_cast<float*>(WS(ICSA_WS_OUTC));
   cp.sharp = reinterpret_cast<float*>(WS(ICSA_WS_SHARP));
-  cp.BH = BH; cp.NB = z.NB; cp.S = S; cp.n_t = z.n_t; cp.k_sparsity = z.k_sparsity;
+  cp.colpart = reinterpret_cast<float*>(WS(ICSA_WS_COLP));
+  cp.rstat = reinterpret_cast<float*>(WS(ICSA_WS_RSTAT));
+  cp.BH = BH; cp.NB = z.NB; cp.S = S; cp.n_t = z.n_t; cp.n_s = z.n_s; cp.k_sparsity = z.k_sparsity;
   ICSA_HIP_TRY(launch_compressed(cp, stream), "compressed attention");
   ICSA_HIP_TRY(mark(ICSA_STAGE_COMPRESSED), "event");
 
@@ -278,7 +283,7 @@ int editing_impl(ICSA_EDITING_ARGS, void* const* stage_events) {
     ICSA_HIP_TRY(hipMemcpyAsync(order, inject_order, (size_t)BH * z.NB * 4, hipMemcpyDeviceToDevice, stream),
                  "inject order");
   SelectParams sp;
-  sp.P = cp.P; sp.sharp = cp.sharp;
+  sp.colpart = cp.colpart; sp.sharp = cp.sharp;
   sp.src_score = reinterpret_cast<float*>(WS(ICSA_WS_SRCSCORE));
   sp.sel = sel; sp.order = order;
   sp.kvmap = reinterpret_cast<int*>(WS(ICSA_WS_KVMAP));
@@ -344,7 +349,7 @@ int editing_impl(ICSA_EDITING_ARGS, void* const* stage_events) {
     } else {
       Level3Params lp;
       lp.qsum = pp.sums[0]; lp.rows = order; lp.rows_offset = z.n_peaked; lp.rows_stride = z.NB;
-      lp.kc32 = np.kc32; lp.idx = l3;
+      lp.kc32 = np.kc32; lp.idx = l3; lp.scores = reinterpret_cast<float*>(WS(ICSA_WS_L3S));
       lp.BH = BH; lp.NQsrc = z.NB; lp.n_rows = z.n_diffuse; lp.NKV = z.NKV; lp.top_k = z.top_k;
       ICSA_HIP_TRY(launch_level3(lp, stream), "level-3 top-k");
     }
@@ -408,7 +413,7 @@ int icsa_editing_sparse_attention_ev(ICSA_EDITING_ARGS, void* const* stage_event
 
 namespace {
 struct SpLayout {
-  int64_t qsum, ksum, vsum, vt, kc32, kc, vct, idx, total;
+  int64_t qsum, ksum, vsum, vt, kc32, kc, vct, idx, scores, total;
 };
 SpLayout sparse_layout(int B, int H, int TQ, int TKV, double sparsity) {
   const int64_t BH = (int64_t)B * H;
@@ -425,6 +430,7 @@ SpLayout sparse_layout(int B, int H, int TQ, int TKV, double sparsity) {
   L.kc = o; o += align256(BH * NKVp * ICSA_D * 2);
   L.vct = o; o += align256(BH * ICSA_D * NKVp * 2);
   L.idx = o; o += align256(BH * NQ * top_k * 4);
+  L.scores = o; o += align256(BH * NQ * (int64_t)NKV * 4);
   L.total = o;
   return L;
 }
@@ -502,7 +508,7 @@ int icsa_sparse_piecewise_attn(
   } else {
     Level3Params lp;
     lp.qsum = pq.sums[0]; lp.rows = nullptr; lp.rows_offset = 0; lp.rows_stride = 0;
-    lp.kc32 = np.kc32; lp.idx = idx;
+    lp.kc32 = np.kc32; lp.idx = idx; lp.scores = reinterpret_cast<float*>(ws + L.scores);
     lp.BH = BH; lp.NQsrc = NQ; lp.n_rows = NQ; lp.NKV = NKV; lp.top_k = top_k;
     ICSA_HIP_TRY(launch_level3(lp, stream), "block top-k");
   }

@@ -12,10 +12,10 @@
 // identical and no float atomics are used.
 #include "icsa_kernels.h"
 
-#define ICSA_MAX_NT 4096     // longest target-column row held in LDS by the softmax kernel
+#define ICSA_MAX_NB 4096     // longest P row held in registers by the strip kernel
 #define ICSA_MAX_SORT 4096   // longest list ranked by the select kernel
-#define ICSA_L3_ROWS 8       // query blocks per workgroup in the level-3 kernel
-#define ICSA_MAX_NKV 2048    // longest level-3 score row held in LDS
+#define ICSA_L3_ROWS 32      // query blocks per workgroup in the level-3 kernel
+#define ICSA_MAX_NKV 2048    // longest level-3 score row held in registers
 
 __device__ __forceinline__ float block_size_f(int blk, int NB, int S) {
   return blk < NB - 1 ? (float)ICSA_BLOCK : (float)(S - (NB - 1) * ICSA_BLOCK);
@@ -74,102 +74,138 @@ __global__ void __launch_bounds__(256) icsa_compressed_logits_kernel(CompressedP
 }
 
 // ---------------------------------------------------------------------------------------
-// (b) row softmax in place + sharpness = sum of the k_sparsity largest P[i, :n_t]
+// (b) row statistics, one wave per row of logits (held in registers, VPL per lane): row
+//     max m, 1 / sum exp(L - m), and the sharpness = sum of the k_sparsity largest
+//     P[i, :n_t].  exp is monotonic, so the k-th largest target probability is
+//     exp(tau - m) / z for the k-th largest target logit tau, found by bisection over the
+//     order-preserving float keys with ballot counts.
 // ---------------------------------------------------------------------------------------
-__device__ __forceinline__ int wave_sum_i(int x) {
+__device__ __forceinline__ int wave_count(bool pred) { return __popcll(__ballot(pred)); }
+
+// Largest key lo with count(key >= lo) >= k over the wave's VPL keys per lane (keys 0 =
+// absent; requires at least k nonzero keys): the key of the k-th largest.
+template <int VPL>
+__device__ __forceinline__ uint32_t kth_largest_key(const uint32_t (&key)[VPL], int k) {
+  uint32_t lo = 0u, hi = 0xffffffffu;
+  while (hi - lo > 1u) {
+    const uint32_t mid = lo + ((hi - lo) >> 1);
+    int c = 0;
 #pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o, 64);
-  return x;
+    for (int u = 0; u < VPL; ++u) c += wave_count(key[u] >= mid);
+    if (c >= k) lo = mid; else hi = mid;
+  }
+  return lo;
 }
 
-__global__ void __launch_bounds__(256) icsa_compressed_softmax_kernel(CompressedParams p) {
-  __shared__ float tgt[4][ICSA_MAX_NT];
+template <int VPL>   // logits per lane: NB <= 64 * VPL
+__global__ void __launch_bounds__(256) icsa_compressed_stats_kernel(CompressedParams p) {
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * 4 + w;
-  const bool active = row < (int64_t)p.BH * p.NB;
-  const int NB = p.NB;
-  const int n_t = p.n_t;
-  if (active) {
-    float* L = p.P + row * NB;
-    float m = -INFINITY;
-    for (int j = lane; j < NB; j += 64) m = fmaxf(m, L[j]);
-    m = wave_max(m);
-    float z = 0.f;
-    for (int j = lane; j < NB; j += 64) z += expf(L[j] - m);
-    z = wave_sum(z);
-    for (int j = lane; j < NB; j += 64) {
-      const float pv = expf(L[j] - m) / z;
-      L[j] = pv;
-      if (j < n_t) tgt[w][j] = pv;
-    }
+  const int64_t row = (int64_t)blockIdx.x * 4 + w;          // over BH * NB rows
+  if (row >= (int64_t)p.BH * p.NB) return;
+  const int NB = p.NB, n_t = p.n_t;
+  const float* L = p.P + row * NB;
+  float v[VPL];
+  float m = -INFINITY;
+#pragma unroll
+  for (int u = 0; u < VPL; ++u) {
+    const int j = lane + 64 * u;
+    v[u] = j < NB ? L[j] : -INFINITY;
+    m = fmaxf(m, v[u]);
   }
-  __syncthreads();
-  if (!active) return;
+  m = wave_max(m);
+  float z = 0.f;
+#pragma unroll
+  for (int u = 0; u < VPL; ++u) z += expf(v[u] - m);
+  z = wave_sum(z);
   float sharp = 0.f;
-  const int k = p.k_sparsity;
   if (n_t > 0) {
-    // largest tau (bit pattern of a non-negative float) with count(P >= tau) >= k
-    uint32_t lo = 0u, hi = 0x7f800000u;
-    while (hi - lo > 1u) {
-      const uint32_t mid = lo + ((hi - lo) >> 1);
-      int c = 0;
-      for (int j = lane; j < n_t; j += 64) c += (__float_as_uint(tgt[w][j]) >= mid) ? 1 : 0;
-      c = wave_sum_i(c);
-      if (c >= k) lo = mid; else hi = mid;
-    }
+    uint32_t key[VPL];
+#pragma unroll
+    for (int u = 0; u < VPL; ++u) key[u] = lane + 64 * u < n_t ? f2key(v[u]) : 0u;
+    const int k = p.k_sparsity;
+    const uint32_t lo = kth_largest_key<VPL>(key, k);
     int cgt = 0;
-    float s = 0.f;
-    for (int j = lane; j < n_t; j += 64) {
-      const float v = tgt[w][j];
-      if (__float_as_uint(v) > lo) { ++cgt; s += v; }
+    float sa = 0.f;
+#pragma unroll
+    for (int u = 0; u < VPL; ++u) {
+      const bool in = key[u] > lo;
+      cgt += wave_count(in);
+      sa += in ? expf(v[u] - m) : 0.f;
     }
-    cgt = wave_sum_i(cgt);
-    s = wave_sum(s);
-    sharp = s + (float)(k - cgt) * __uint_as_float(lo);
+    sa = wave_sum(sa);
+    sharp = (sa + (float)(k - cgt) * expf(key2f(lo) - m)) / z;
   }
-  if (lane == 0) p.sharp[row] = sharp;
+  if (lane == 0) {
+    p.rstat[2 * row] = m;
+    p.rstat[2 * row + 1] = 1.f / z;
+    p.sharp[row] = sharp;
+  }
 }
 
 // ---------------------------------------------------------------------------------------
-// (c) out_c = P (Vs/size), one 64-row tile per workgroup (fp32 MFMA)
+// (c) one 64-row strip of P per workgroup of 8 waves, in 64-column chunks: P = exp(L - m)/z
+//     written in place, out_c += P (Vs/size) with fp32 MFMA (wave w: rows 32 (w & 1),
+//     columns 32 (w >> 1)), and for strips holding target rows the column sums of the
+//     source columns over those rows (partials in strip order, summed by the select kernel).
 // ---------------------------------------------------------------------------------------
-__global__ void __launch_bounds__(256) icsa_compressed_pv_kernel(CompressedParams p) {
+__global__ void __launch_bounds__(512) icsa_compressed_rows_kernel(CompressedParams p) {
   __shared__ float ps[64][68];
   __shared__ float vs[64][132];
-  const int rt = blockIdx.x, bh = blockIdx.y;
-  const int NB = p.NB;
-  const float* P = p.P + (int64_t)bh * NB * NB;
+  __shared__ float row_m[64], row_iz[64];
+  const int strip = blockIdx.x, bh = blockIdx.y;
+  const int NB = p.NB, n_t = p.n_t;
+  const int r_base = strip * 64;
+  float* Pbh = p.P + (int64_t)bh * NB * NB;
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  if (tid < 64) {
+    const int row = r_base + tid;
+    row_m[tid] = row < NB ? p.rstat[2 * ((int64_t)bh * NB + row)] : 0.f;
+    row_iz[tid] = row < NB ? p.rstat[2 * ((int64_t)bh * NB + row) + 1] : 0.f;
+  }
   const float* V = p.vsum + (int64_t)bh * NB * ICSA_D;
-  const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
-  const int li = l & 31, hl = l >> 5;
-  const int r0 = 32 * (w & 1), c0 = 64 * (w >> 1);
-  floatx16 acc0 = {}, acc1 = {};
+  const int li = lane & 31, hl = lane >> 5;
+  const int r0 = 32 * (w & 1), c0 = 32 * (w >> 1);
+  const int n_ts = (n_t + ICSA_BLOCK - 1) / ICSA_BLOCK;
+  const int tgt_rows = min(64, n_t - r_base);          // > 0 only for target strips
+  floatx16 acc = {};
+  __syncthreads();
   for (int k0 = 0; k0 < NB; k0 += 64) {
-    for (int e = threadIdx.x; e < 64 * 64; e += 256) {
+    for (int e = tid; e < 64 * 64; e += 512) {
       const int r = e >> 6, kk = e & 63;
-      const int row = rt * 64 + r, kc = k0 + kk;
-      ps[r][kk] = (row < NB && kc < NB) ? P[(int64_t)row * NB + kc] : 0.f;
+      const int row = r_base + r, col = k0 + kk;
+      float pv = 0.f;
+      if (row < NB && col < NB) {
+        float* Lp = Pbh + (int64_t)row * NB + col;
+        pv = expf(*Lp - row_m[r]) * row_iz[r];
+        *Lp = pv;
+      }
+      ps[r][kk] = pv;
     }
-    for (int e = threadIdx.x; e < 64 * 32; e += 256) {
+    for (int e = tid; e < 64 * 32; e += 512) {
       const int kk = e >> 5, c4 = e & 31;
       const int kc = k0 + kk;
-      floatx4 v = {0.f, 0.f, 0.f, 0.f};
+      floatx4 vv = {0.f, 0.f, 0.f, 0.f};
       if (kc < NB) {
-        v = *reinterpret_cast<const floatx4*>(V + (int64_t)kc * ICSA_D + 4 * c4);
-        const float sz = block_size_f(kc, NB, p.S);
+        vv = *reinterpret_cast<const floatx4*>(V + (int64_t)kc * ICSA_D + 4 * c4);
+        const float inv = 1.f / block_size_f(kc, NB, p.S);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] = v[i] / sz;
+        for (int i = 0; i < 4; ++i) vv[i] *= inv;
       }
-      *reinterpret_cast<floatx4*>(&vs[kk][4 * c4]) = v;
+      *reinterpret_cast<floatx4*>(&vs[kk][4 * c4]) = vv;
     }
     __syncthreads();
 #pragma unroll 2
     for (int s = 0; s < 32; s += 4) {
       const floatx4 a = *reinterpret_cast<const floatx4*>(&ps[r0 + li][32 * hl + s]);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        acc0 = mfma32x32x2f32(a[j], vs[32 * hl + s + j][c0 + li], acc0);
-        acc1 = mfma32x32x2f32(a[j], vs[32 * hl + s + j][c0 + 32 + li], acc1);
+      for (int j = 0; j < 4; ++j) acc = mfma32x32x2f32(a[j], vs[32 * hl + s + j][c0 + li], acc);
+    }
+    if (tgt_rows > 0 && k0 + 64 > n_t && tid < 64) {
+      const int col = k0 + tid;
+      if (col >= n_t && col < NB) {
+        float cs = 0.f;
+        for (int r = 0; r < tgt_rows; ++r) cs += ps[r][tid];
+        p.colpart[((int64_t)bh * n_ts + strip) * p.n_s + (col - n_t)] = cs;
       }
     }
     __syncthreads();
@@ -177,26 +213,32 @@ __global__ void __launch_bounds__(256) icsa_compressed_pv_kernel(CompressedParam
   float* out = p.out_c + (int64_t)bh * NB * ICSA_D;
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
-    const int row = rt * 64 + r0 + acc_row(i, l);
-    if (row < NB) {
-      out[(int64_t)row * ICSA_D + c0 + li] = acc0[i];
-      out[(int64_t)row * ICSA_D + c0 + 32 + li] = acc1[i];
-    }
+    const int row = r_base + r0 + acc_row(i, lane);
+    if (row < NB) out[(int64_t)row * ICSA_D + c0 + li] = acc[i];
   }
 }
 
 hipError_t launch_compressed(const CompressedParams& p, hipStream_t stream) {
-  if (p.n_t > ICSA_MAX_NT) return hipErrorInvalidValue;
+  if (p.NB > ICSA_MAX_NB) return hipErrorInvalidValue;
   const int nt = (p.NB + 63) / 64;
   hipLaunchKernelGGL(icsa_compressed_logits_kernel, dim3(nt, nt, p.BH), dim3(256), 0, stream, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int64_t rows = (int64_t)p.BH * p.NB;
-  hipLaunchKernelGGL(icsa_compressed_softmax_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0,
-                     stream, p);
+  const dim3 sgrid((unsigned)((rows + 3) / 4));
+  if (p.NB <= 256)
+    hipLaunchKernelGGL(icsa_compressed_stats_kernel<4>, sgrid, dim3(256), 0, stream, p);
+  else if (p.NB <= 512)
+    hipLaunchKernelGGL(icsa_compressed_stats_kernel<8>, sgrid, dim3(256), 0, stream, p);
+  else if (p.NB <= 1024)
+    hipLaunchKernelGGL(icsa_compressed_stats_kernel<16>, sgrid, dim3(256), 0, stream, p);
+  else if (p.NB <= 2048)
+    hipLaunchKernelGGL(icsa_compressed_stats_kernel<32>, sgrid, dim3(256), 0, stream, p);
+  else
+    hipLaunchKernelGGL(icsa_compressed_stats_kernel<64>, sgrid, dim3(256), 0, stream, p);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(icsa_compressed_pv_kernel, dim3(nt, p.BH), dim3(256), 0, stream, p);
+  hipLaunchKernelGGL(icsa_compressed_rows_kernel, dim3(nt, p.BH), dim3(512), 0, stream, p);
   return hipGetLastError();
 }
 
@@ -231,23 +273,16 @@ __global__ void __launch_bounds__(1024) icsa_select_kernel(SelectParams p) {
   __shared__ int sel_l[ICSA_MAX_SORT];
   const int bh = blockIdx.x;
   const int NB = p.NB, n_t = p.n_t, n_s = p.n_s;
-  const float* P = p.P + (int64_t)bh * NB * NB;
   int n1 = 1;
   while (n1 < n_s) n1 <<= 1;
-  // column mass of source key blocks over target query blocks, sequential over rows
+  // column mass of source key blocks over target query blocks: the per-strip partial
+  // sums of the strip kernel, added in strip order
+  const int n_ts = (n_t + ICSA_BLOCK - 1) / ICSA_BLOCK;
+  const float* part = p.colpart + (int64_t)bh * n_ts * n_s;
   for (int j = threadIdx.x; j < n1; j += blockDim.x) {
     if (j < n_s) {
       float s = 0.f;
-      const float* col = P + n_t + j;
-      int i = 0;
-      for (; i + 8 <= n_t; i += 8) {
-        float v[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) v[u] = col[(int64_t)(i + u) * NB];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) s += v[u];
-      }
-      for (; i < n_t; ++i) s += col[(int64_t)i * NB];
+      for (int st = 0; st < n_ts; ++st) s += part[(int64_t)st * n_s + j];
       p.src_score[(int64_t)bh * n_s + j] = s;
       keys[j] = rank_key(s, j);
     } else {
@@ -317,83 +352,109 @@ hipError_t launch_newkv_sums(const NewKvSumsParams& p, hipStream_t stream) {
 }
 
 // ---------------------------------------------------------------------------------------
-// (f) level-3: per query block, top_k new-KV blocks by QCsum . KCsum (fp32), ascending list
+// (f) level-3: per query block, top_k new-KV blocks by QCsum . KCsum (fp32), ascending list.
+//     Scores: 32 query blocks per workgroup, fp32 MFMA over 64-block chunks, written to a
+//     scratch row per query block.  Selection: one wave per query block, bisection over the
+//     float keys (ballot counts), then compaction in ascending block order.
 // ---------------------------------------------------------------------------------------
-__global__ void __launch_bounds__(256) icsa_level3_kernel(Level3Params p) {
-  __shared__ float qrow[ICSA_L3_ROWS][ICSA_D];
-  __shared__ float sc[ICSA_L3_ROWS][ICSA_MAX_NKV];
+__global__ void __launch_bounds__(128) icsa_level3_scores_kernel(Level3Params p) {
+  __shared__ float qs[ICSA_L3_ROWS][132];
+  __shared__ float ks[64][132];
   const int bh = blockIdx.y;
-  const int r0 = blockIdx.x * ICSA_L3_ROWS;
+  const int r_base = blockIdx.x * ICSA_L3_ROWS;
   const int NKV = p.NKV;
-  for (int e = threadIdx.x; e < ICSA_L3_ROWS * ICSA_D; e += 256) {
-    const int r = e / ICSA_D, d = e % ICSA_D;
-    float v = 0.f;
-    if (r0 + r < p.n_rows) {
-      const int qb = p.rows ? p.rows[(int64_t)bh * p.rows_stride + p.rows_offset + r0 + r] : r0 + r;
-      v = p.qsum[((int64_t)bh * p.NQsrc + qb) * ICSA_D + d];
-    }
-    qrow[r][d] = v;
-  }
-  __syncthreads();
-  const float* kc = p.kc32 + (int64_t)bh * NKV * ICSA_D;
-  for (int j = threadIdx.x; j < NKV; j += 256) {
-    float acc[ICSA_L3_ROWS];
-#pragma unroll
-    for (int r = 0; r < ICSA_L3_ROWS; ++r) acc[r] = 0.f;
-    for (int d = 0; d < ICSA_D; d += 4) {
-      const floatx4 kv = *reinterpret_cast<const floatx4*>(kc + (int64_t)j * ICSA_D + d);
-#pragma unroll
-      for (int r = 0; r < ICSA_L3_ROWS; ++r) {
-#pragma unroll
-        for (int u = 0; u < 4; ++u) acc[r] = fmaf(qrow[r][d + u], kv[u], acc[r]);
-      }
-    }
-#pragma unroll
-    for (int r = 0; r < ICSA_L3_ROWS; ++r) sc[r][j] = acc[r];
-  }
-  __syncthreads();
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int k = p.top_k;
+  const int li = lane & 31, hl = lane >> 5;
+  for (int e = threadIdx.x; e < ICSA_L3_ROWS * 32; e += 128) {
+    const int r = e >> 5, c4 = e & 31;
+    floatx4 qv = {0.f, 0.f, 0.f, 0.f};
+    if (r_base + r < p.n_rows) {
+      const int qb = p.rows ? p.rows[(int64_t)bh * p.rows_stride + p.rows_offset + r_base + r] : r_base + r;
+      qv = *reinterpret_cast<const floatx4*>(p.qsum + ((int64_t)bh * p.NQsrc + qb) * ICSA_D + 4 * c4);
+    }
+    *reinterpret_cast<floatx4*>(&qs[r][4 * c4]) = qv;
+  }
+  const float* kc = p.kc32 + (int64_t)bh * NKV * ICSA_D;
+  float* sc = p.scores + ((int64_t)bh * p.n_rows + r_base) * NKV;
+  for (int k0 = 0; k0 < NKV; k0 += 64) {
+    __syncthreads();                              // q rows ready / previous chunk consumed
+    for (int e = threadIdx.x; e < 64 * 32; e += 128) {
+      const int r = e >> 5, c4 = e & 31;
+      floatx4 kv = {0.f, 0.f, 0.f, 0.f};
+      if (k0 + r < NKV) kv = *reinterpret_cast<const floatx4*>(kc + (int64_t)(k0 + r) * ICSA_D + 4 * c4);
+      *reinterpret_cast<floatx4*>(&ks[r][4 * c4]) = kv;
+    }
+    __syncthreads();
+    floatx16 acc = {};
+#pragma unroll 4
+    for (int kk = 0; kk < 64; kk += 4) {
+      const floatx4 a = *reinterpret_cast<const floatx4*>(&qs[li][64 * hl + kk]);
+      const floatx4 b = *reinterpret_cast<const floatx4*>(&ks[32 * w + li][64 * hl + kk]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc = mfma32x32x2f32(a[j], b[j], acc);
+    }
+    const int blk = k0 + 32 * w + li;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int row = acc_row(i, lane);
+      if (r_base + row < p.n_rows && blk < NKV) sc[(int64_t)row * NKV + blk] = acc[i];
+    }
+  }
+}
+
+template <int VPL>   // scores per lane: NKV <= 64 * VPL
+__global__ void __launch_bounds__(256) icsa_level3_select_kernel(Level3Params p) {
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + w;          // over BH * n_rows
+  if (row >= (int64_t)p.BH * p.n_rows) return;
+  const int NKV = p.NKV, k = p.top_k;
+  const float* srow = p.scores + row * NKV;
+  uint32_t key[VPL];
+#pragma unroll
+  for (int u = 0; u < VPL; ++u) {
+    const int j = lane + 64 * u;
+    key[u] = j < NKV ? f2key(srow[j]) : 0u;         // 0 is below every real key
+  }
+  const uint32_t lo = kth_largest_key<VPL>(key, k);
+  int cgt = 0;
+#pragma unroll
+  for (int u = 0; u < VPL; ++u) cgt += wave_count(key[u] > lo);
+  const int need_eq = k - cgt;
   const unsigned long long lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  for (int rr = w; rr < ICSA_L3_ROWS; rr += 4) {
-    const int r = r0 + rr;
-    if (r >= p.n_rows) break;
-    // largest key tau with count(key >= tau) >= k
-    uint32_t lo = 0u, hi = 0xffffffffu;
-    while (hi - lo > 1u) {
-      const uint32_t mid = lo + ((hi - lo) >> 1);
-      int c = 0;
-      for (int j = lane; j < NKV; j += 64) c += (f2key(sc[rr][j]) >= mid) ? 1 : 0;
-      c = wave_sum_i(c);
-      if (c >= k) lo = mid; else hi = mid;
-    }
-    int cgt = 0;
-    for (int j = lane; j < NKV; j += 64) cgt += (f2key(sc[rr][j]) > lo) ? 1 : 0;
-    cgt = wave_sum_i(cgt);
-    const int need_eq = k - cgt;
-    int seen_eq = 0, taken = 0;
-    int* out = p.idx + ((int64_t)bh * p.n_rows + r) * k;
-    for (int base = 0; base < NKV; base += 64) {
-      const int j = base + lane;
-      uint32_t key = 0u;
-      if (j < NKV) key = f2key(sc[rr][j]);
-      const bool gt = (j < NKV) && key > lo;
-      const bool eq = (j < NKV) && key == lo;
-      const unsigned long long eqm = __ballot(eq);
-      const int eq_before = seen_eq + __popcll(eqm & lt_mask);
-      const bool take = gt || (eq && eq_before < need_eq);
-      const unsigned long long tm = __ballot(take);
-      const int pos = taken + __popcll(tm & lt_mask);
-      if (take && pos < k) out[pos] = j;
-      seen_eq += __popcll(eqm);
-      taken += __popcll(tm);
-    }
+  int seen_eq = 0, taken = 0;
+  int* out = p.idx + row * k;
+#pragma unroll
+  for (int u = 0; u < VPL; ++u) {
+    const int j = lane + 64 * u;
+    const bool gt = key[u] > lo;
+    const bool eq = key[u] == lo && j < NKV;
+    const unsigned long long eqm = __ballot(eq);
+    const int eq_before = seen_eq + __popcll(eqm & lt_mask);
+    const bool take = gt || (eq && eq_before < need_eq);
+    const unsigned long long tm = __ballot(take);
+    const int pos = taken + __popcll(tm & lt_mask);
+    if (take && pos < k) out[pos] = j;
+    seen_eq += __popcll(eqm);
+    taken += __popcll(tm);
   }
 }
 
 hipError_t launch_level3(const Level3Params& p, hipStream_t stream) {
   if (p.NKV > ICSA_MAX_NKV || p.top_k > p.NKV || p.top_k < 1) return hipErrorInvalidValue;
-  dim3 grid((p.n_rows + ICSA_L3_ROWS - 1) / ICSA_L3_ROWS, p.BH);
-  hipLaunchKernelGGL(icsa_level3_kernel, grid, dim3(256), 0, stream, p);
+  if (p.n_rows <= 0) return hipSuccess;
+  hipLaunchKernelGGL(icsa_level3_scores_kernel, dim3((p.n_rows + ICSA_L3_ROWS - 1) / ICSA_L3_ROWS, p.BH),
+                     dim3(128), 0, stream, p);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const int64_t rows = (int64_t)p.BH * p.n_rows;
+  const dim3 grid((unsigned)((rows + 3) / 4));
+  if (p.NKV <= 256)
+    hipLaunchKernelGGL(icsa_level3_select_kernel<4>, grid, dim3(256), 0, stream, p);
+  else if (p.NKV <= 512)
+    hipLaunchKernelGGL(icsa_level3_select_kernel<8>, grid, dim3(256), 0, stream, p);
+  else if (p.NKV <= 1024)
+    hipLaunchKernelGGL(icsa_level3_select_kernel<16>, grid, dim3(256), 0, stream, p);
+  else
+    hipLaunchKernelGGL(icsa_level3_select_kernel<32>, grid, dim3(256), 0, stream, p);
   return hipGetLastError();
 }

@@ -25,13 +25,15 @@ struct CompressedParams {
   float* P;             // [BH, NB, NB] logits, then softmax probabilities in place
   float* out_c;         // [BH, NB, D]
   float* sharp;         // [BH, NB]
+  float* colpart;       // [BH, ceil(n_t/64), n_s] source-column sums per 64-row target strip
+  float* rstat;         // [BH, NB, 2] row max, 1 / row sum of exp
   int BH, NB, S;        // S: tokens (last block size = S - (NB-1)*64)
-  int n_t, k_sparsity;
+  int n_t, n_s, k_sparsity;
 };
 hipError_t launch_compressed(const CompressedParams& p, hipStream_t stream);
 
 struct SelectParams {
-  const float* P;       // [BH, NB, NB]
+  const float* colpart; // [BH, ceil(n_t/64), n_s] (CompressedParams::colpart)
   const float* sharp;   // [BH, NB]
   float* src_score;     // [BH, n_s]
   int* sel;             // [BH, topK]   (ranked order)
@@ -61,6 +63,7 @@ struct Level3Params {
   int rows_offset, rows_stride;
   const float* kc32;    // [BH, NKV, D]
   int* idx;             // [BH, n_rows, top_k]  ascending block indices
+  float* scores;        // [BH, n_rows, NKV]  scratch
   int BH, NQsrc, n_rows, NKV, top_k;
 };
 hipError_t launch_level3(const Level3Params& p, hipStream_t stream);
