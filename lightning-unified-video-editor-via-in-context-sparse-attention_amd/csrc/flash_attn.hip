@@ -144,6 +144,7 @@ icsa_flash_kernel(FlashParams p) {
   // from LDS into registers FA_PF MFMA steps ahead of their use (explicit software
   // pipeline), so the matrix pipe does not wait on LDS latency.
   auto gemm = [&](int k) {
+    __builtin_amdgcn_s_setprio(1);              // the matrix-feeding wave wins issue ties
     if (k >= 1) {
       const unsigned char* vs = vbuf((k - 1) & 1);
       bf16x8 va[16];
@@ -182,6 +183,7 @@ icsa_flash_kernel(FlashParams p) {
       s[0] = acc0;
       s[1] = acc1;
     }
+    __builtin_amdgcn_s_setprio(0);
   };
   // SOFT(k): mask, row max, lazy rescale, P(k)
   auto soft = [&](int k) {
