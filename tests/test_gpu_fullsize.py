@@ -1,0 +1,120 @@
+"""Parity at the benchmark sizes (65,536 and 65,520 tokens, H = 40, D = 128).
+
+The whole CPU oracle is too slow at this size, so the check is split by stage, each
+part against float64 arithmetic on the same bf16 inputs:
+
+* block sums and the compressed softmax P: the oracle's functions, run in float64;
+* every ranked decision -- source blocks, the peaked/diffuse split, the per-block exact
+  lists -- must be a valid ranking of the float64 scores within GAP;
+* a sample of output rows (peaked and diffuse query blocks of several heads) against
+  float64 attention for exactly those blocks, built from the GPU's own decisions;
+* size-independent properties: two runs are bit-identical, and x is exactly linear in
+  alpha_2 (x(alpha) - x(0) = alpha * out_c).
+"""
+import math
+
+import pytest
+import torch
+
+import oracle as O
+from in_context_sparse_attention.editing_sparse_attention import _editing_sparse_attention_hip
+from in_context_sparse_attention.synthetic import make_inputs
+from parity import GAP, MAX_ABS, MEAN_ABS, l3_scale
+
+pytestmark = pytest.mark.gpu
+
+CASES = {
+    "cfg2": dict(H=40, real=32760, pad=8, kind="random", seed=0),
+    "cfg3": dict(H=40, real=32760, pad=8, kind="structured", seed=0),
+    "unaligned": dict(H=40, real=32760, pad=0, kind="random", seed=7),
+}
+
+
+def _block_sums(x, NB):
+    """float64 [B, H, NB, D] sums of the 64-token blocks of x [B, S, H, D] (zero padded)."""
+    B, S, H, D = x.shape
+    xp = torch.zeros(B, NB * 64, H, D, dtype=torch.float64, device=x.device)
+    xp[:, :S] = x.double()
+    return xp.view(B, NB, 64, H, D).sum(2).permute(0, 2, 1, 3)
+
+
+@pytest.mark.parametrize("case", list(CASES))
+def test_full_size_parity(gpu, case):
+    print(f"[fullsize] {case}: generating inputs", flush=True)
+    q, k, v, t = make_inputs(**CASES[case], device=gpu)
+    B, S, H, D = q.shape
+    g = torch.Generator(device=gpu).manual_seed(11)
+    alpha = (torch.rand(B, S, 1, 1, device=gpu, generator=g) - 0.5) * 0.5
+    x, views = _editing_sparse_attention_hip(q, k, v, t, alpha, keep_workspace=True)
+    x_again, _ = _editing_sparse_attention_hip(q, k, v, t, alpha)
+    x0, _ = _editing_sparse_attention_hip(q, k, v, t, 0.0)
+    torch.cuda.synchronize()
+    z = O.derive_sizes(B, S, H, D, t)
+    print(f"[fullsize] {case}: S={S} t={t} sizes={z}", flush=True)
+    assert torch.equal(x, x_again), "two runs differ"
+    assert torch.isfinite(x.float()).all()
+
+    # ---- stage 1 and the compressed softmax ----
+    NB = z.NB
+    sizes = O.block_sizes(S).to(device=gpu, dtype=torch.float64).view(1, 1, NB, 1)
+    qs, ks, vs = _block_sums(q, NB), _block_sums(k, NB), _block_sums(v, NB)
+    assert torch.allclose(views["q_sums"].double(), qs, rtol=1e-5, atol=1e-3)
+    assert torch.allclose(views["v_sums"].double(), vs, rtol=1e-5, atol=1e-3)
+    P, out_c = O.compressed_attention(qs / sizes, ks / sizes, vs / sizes)
+    assert torch.allclose(views["P"].double(), P, rtol=1e-4, atol=1e-7)
+    assert torch.allclose(views["out_c"].double(), out_c, rtol=1e-4, atol=1e-5)
+    # exact linearity in alpha_2 on every token
+    oc = out_c.float().repeat_interleave(64, dim=2).permute(0, 2, 1, 3)[:, :S]
+    d = (x.float() - x0.float()) - alpha * oc
+    assert d.abs().max().item() <= 2e-2 and d.abs().mean().item() <= 1e-3
+
+    # ---- decisions ----
+    sel = views["sel"].long()
+    order = views["order"].long()
+    peaked, diffuse = order[..., :z.n_peaked], order[..., z.n_peaked:]
+    _, src_score = O.select_source_blocks(P, z.n_t, z.topK)
+    assert O.check_topk_valid(src_score, sel, z.topK, GAP, ordered=True).all()
+    _, _, sharp = O.split_blocks(P, z.n_t, z.k_sparsity, z.n_peaked)
+    assert O.check_split_valid(sharp, peaked, GAP).all()
+    # new KV (GPU selection, closed-form token map) and its block sums
+    tokmap = O.new_kv_token_map(t, S, sel.cpu()).to(gpu)             # [B, H, Tkv]
+    pad = z.TKV_pad - z.Tkv
+    kh, vh = k.permute(0, 2, 1, 3), v.permute(0, 2, 1, 3)
+    idx = tokmap.clamp(min=0)[..., None].expand(-1, -1, -1, D)
+    nk = torch.gather(kh, 2, idx).masked_fill((tokmap < 0)[..., None], 0)
+    nv = torch.gather(vh, 2, idx).masked_fill((tokmap < 0)[..., None], 0)
+    nk = torch.nn.functional.pad(nk, (0, 0, 0, pad))
+    nv = torch.nn.functional.pad(nv, (0, 0, 0, pad))
+    kc = nk.double().view(B, H, z.NKV, 64, D).sum(3)
+    bi, hi = torch.arange(B, device=gpu).view(B, 1, 1), torch.arange(H, device=gpu).view(1, H, 1)
+    qc = qs[bi, hi, diffuse]
+    l3_scores = torch.matmul(qc, kc.transpose(-1, -2))
+    l3 = views["l3"].long()
+    assert O.check_topk_valid(l3_scores / l3_scale(D), l3, z.top_k, GAP, ordered=False).all()
+    print(f"[fullsize] {case}: decisions valid", flush=True)
+
+    # ---- sampled output blocks, float64 ----
+    errs = []
+    for h in (0, 13, 27, H - 1):
+        for kind, blocks in (("peaked", peaked[0, h, :2]), ("diffuse", diffuse[0, h, :2])):
+            for blk in blocks.tolist():
+                r0, r1 = 64 * blk, min(S, 64 * blk + 64)
+                qb = torch.zeros(64, D, dtype=torch.float64, device=gpu)
+                qb[:r1 - r0] = q[0, r0:r1, h].double()
+                if kind == "peaked":
+                    kk, vv = nk[0, h, :z.Tkv].double(), nv[0, h, :z.Tkv].double()
+                    s = qb @ kk.T / math.sqrt(D)
+                    ob = torch.softmax(s, -1) @ vv
+                else:
+                    pos = (diffuse[0, h] == blk).nonzero()[0, 0].item()
+                    ob, _, _ = O.sparse_piecewise_attn(
+                        qb.cpu().view(1, 1, 64, D), nk[0, h].cpu().view(1, 1, -1, D),
+                        nv[0, h].cpu().view(1, 1, -1, D), 0.0625,
+                        indices=l3[0, h, pos].cpu().view(1, 1, 1, -1))
+                    ob = ob.view(64, D).to(gpu)
+                ref = ob[:r1 - r0] + alpha[0, r0:r1, 0].double() * out_c[0, h, blk].view(1, D)
+                errs.append((x[0, r0:r1, h].double() - ref).abs())
+    e = torch.cat(errs)
+    print(f"[fullsize] {case}: sampled rows max_abs={e.max().item():.3e} mean_abs={e.mean().item():.3e}",
+          flush=True)
+    assert e.max().item() <= MAX_ABS and e.mean().item() <= MEAN_ABS
