@@ -72,6 +72,9 @@ CONFIGS = {
     2: dict(H=40, real=32760, pad=8, kind="random"),
     # structured scores, 21 frames x 1560 tokens per part
     3: dict(H=40, real=32760, pad=8, kind="structured"),
+    # the DiT block's attention call, 65,520 unpadded tokens (t = 32,760,
+    # t % 64 != 0 and a partial last block)
+    4: dict(H=40, real=32760, pad=0, kind="random"),
 }
 
 
