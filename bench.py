@@ -96,8 +96,8 @@ def cpu_baseline(seconds):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=10)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", type=int, default=2, choices=[2, 3, 4],
                     help="2: 65,536 random tokens (headline); 3: structured; 4: 65,520 tokens "
                          "(unaligned t, the DiT block's attention call)")
