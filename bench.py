@@ -93,6 +93,114 @@ def cpu_baseline(seconds):
     }
 
 
+def reference_glue(yq, yk, al, wq, wk, grid, freqs, H, eps=1e-6):
+    """The reference's own producer of the attention inputs, restated in PyTorch on the GPU
+    for timing: WanRMSNorm in fp32 with the bf16 round trip (model.py:103-114), the alpha_1
+    gate in bf16 (model.py:162) and rope_apply's float64 complex product (model.py:69-95)
+    for one batch element with TAG == 1 and the same grid for target and source.  Returns
+    fp32 q, k [1, S, H, D] and the bf16 gate, which the reference hands to
+    editing_sparse_attention."""
+    import torch
+    B, S, dim = yq.shape
+    D = dim // H
+
+    def rms(y, w):
+        x = y.float()
+        return (x * torch.rsqrt(x.pow(2).mean(dim=-1, keepdim=True) + eps)).type_as(y) * w
+
+    c = D // 2
+    f, h, w_ = grid
+    fr = freqs.to(yq.device).split([c - 2 * (c // 3), c // 3, c // 3], dim=1)
+    grid_freqs = torch.cat([fr[0][:f].view(f, 1, 1, -1).expand(f, h, w_, -1),
+                            fr[1][:h].view(1, h, 1, -1).expand(f, h, w_, -1),
+                            fr[2][:w_].view(1, 1, w_, -1).expand(f, h, w_, -1)],
+                           dim=-1).reshape(f * h * w_, 1, -1)
+    freqs_i = torch.cat([grid_freqs, grid_freqs], dim=0)
+    if freqs_i.shape[0] < S:
+        freqs_i = torch.cat([freqs_i, torch.ones(S - freqs_i.shape[0], 1, c, dtype=freqs_i.dtype,
+                                                 device=freqs_i.device)], dim=0)
+
+    def rope(x):
+        xc = torch.view_as_complex(x[0].to(torch.float64).reshape(S, H, -1, 2))
+        return torch.view_as_real(xc * freqs_i).flatten(2).unsqueeze(0).float()
+
+    q = rope(rms(yq, wq).view(B, S, H, D))
+    k = rope(rms(yk, wk).view(B, S, H, D))
+    gate = (al.view(B, S, 1, 1).sigmoid() - 0.5) * 0.5
+    return q, k, gate
+
+
+def wan_attention_bench(steps, warmup, log_fn):
+    """Configuration 4's attention call inside WanSelfAttention.forward (21x30x52 target and
+    source grids, 65,520 tokens, H = 40): from the q / k / v / alpha_1 projections to the
+    attention output, (a) through this build's fused producer + attention core and (b)
+    through the reference's glue (fp32 RMSNorm, float64 RoPE) feeding the same attention."""
+    import torch
+    from in_context_sparse_attention import editing_sparse_attention, wan
+    dev = torch.device("cuda:0")
+    B, H, D = 1, 40, 128
+    grid = (21, 30, 52)
+    S = 2 * grid[0] * grid[1] * grid[2]
+    t = S // 2
+    dim = H * D
+    g = torch.Generator(device=dev).manual_seed(0)
+    yq = torch.randn(B, S, dim, device=dev, generator=g).to(torch.bfloat16)
+    yk = torch.randn(B, S, dim, device=dev, generator=g).to(torch.bfloat16)
+    yv = torch.randn(B, S, dim, device=dev, generator=g).to(torch.bfloat16)
+    al = torch.randn(B, S, 1, device=dev, generator=g).to(torch.bfloat16)
+    wq = torch.rand(dim, device=dev, generator=g) + 0.5
+    wk = torch.rand(dim, device=dev, generator=g) + 0.5
+    freqs = wan.wan_freqs(D)
+    stream = torch.cuda.current_stream(dev)
+
+    def timed(fn, n):
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(n)]
+        for a, b in ev:
+            a.record(stream)
+            fn()
+            b.record(stream)
+        torch.cuda.synchronize()
+        return statistics.mean(a.elapsed_time(b) for a, b in ev)
+
+    def producer():
+        wan.wan_qk_prologue(yq, yk, wq, wk, [grid], [grid], 1, freqs, H, alpha_logit=al)
+
+    def fused():
+        wan.wan_self_attention_core(yq, yk, yv, al, wq, wk, [grid], [grid], 1, freqs, H)
+
+    def ref_glue():
+        reference_glue(yq, yk, al, wq, wk, grid, freqs, H)
+
+    qr, kr, gr = reference_glue(yq, yk, al, wq, wk, grid, freqs, H)
+    v4 = yv.view(B, S, H, D)
+
+    def ref_attention():
+        editing_sparse_attention(qr, kr, v4, t, S - t, alpha_2=gr, backend="hip")
+
+    for fn in (producer, fused, ref_glue, ref_attention):
+        for _ in range(warmup):
+            fn()
+    torch.cuda.synchronize()
+    n = max(3, steps // 2)
+    res = {"producer_ms": timed(producer, n), "fused_ms": timed(fused, n),
+           "reference_glue_ms": timed(ref_glue, n), "attention_fp32_qk_ms": timed(ref_attention, n)}
+    res["reference_total_ms"] = res["reference_glue_ms"] + res["attention_fp32_qk_ms"]
+    res["speedup_vs_reference_glue"] = res["reference_total_ms"] / res["fused_ms"]
+    NB = (S + 63) // 64
+    alg = 2 * (B * S * dim * 2) * 2 + 2 * (B * H * NB * D * 4) + B * S * (2 + 4)
+    res["producer_bytes"] = alg
+    res["producer_hbm_gbps"] = alg / res["producer_ms"] / 1e6
+    res["workload"] = (f"configuration 4 attention call: B={B} S={S} (t={t}, grids {grid} + {grid}), "
+                       f"H={H} D={D}, bf16 projections, SAR 0.0625, flat 0.5")
+    log_fn(f"[bench] wan attention call: fused {res['fused_ms']:.3f} ms (producer "
+           f"{res['producer_ms']:.3f} ms, {res['producer_hbm_gbps']:.0f} GB/s); reference glue "
+           f"{res['reference_glue_ms']:.3f} ms + attention on fp32 q/k {res['attention_fp32_qk_ms']:.3f} ms")
+    del yq, yk, yv, qr, kr
+    torch.cuda.empty_cache()
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -106,6 +214,11 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-dense", action="store_true")
+    ap.add_argument("--no-wan", action="store_true",
+                    help="skip the configuration-4 WanSelfAttention leg (fused producer vs the "
+                         "reference's glue)")
+    ap.add_argument("--wan-only", action="store_true",
+                    help="run only the configuration-4 WanSelfAttention leg (for profiling)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
                     help="after the timed steps, run 3 elementwise copies (torch.neg) of BYTES "
                          "bytes: the reference kernel of known traffic that scales the HBM "
@@ -125,6 +238,9 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     _lib.lib()
+    if args.wan_only:
+        print(json.dumps({"wan_attention": wan_attention_bench(args.steps, args.warmup, log)}), flush=True)
+        return
     q, k, v, t = config_inputs(args.config, device=dev)
     B, S, H, D = q.shape
     z = derived_sizes(B, S, H, D, t, args.sar, 0.125, args.flat_ratio)
@@ -249,6 +365,10 @@ def main():
                      "kernel": "icsa_flash_kernel (peaked query blocks)",
                      "flops_per_launch": fa_flops},
     }
+    if not args.no_wan:
+        del q, k, v
+        torch.cuda.empty_cache()
+        result["wan_attention"] = wan_attention_bench(args.steps, args.warmup, log)
     if not args.no_cpu_baseline:
         cb = cpu_baseline(args.cpu_seconds)
         log(f"[bench] cpu baseline: {cb['sample']} on {cb['cores']} threads")

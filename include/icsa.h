@@ -30,6 +30,13 @@
  *                                        and compress_seq :37-55 (sums; means = sums / size)
  *   icsa_gather_kv                  <- new_k / new_v construction,
  *                                        editing_sparse_attention.py:138-159
+ *   icsa_wan_qk_prologue            <- the q / k producer of WanSelfAttention.forward,
+ *                                        model.py:156-171: WanRMSNorm (model.py:103-114),
+ *                                        rope_apply (model.py:69-95), alpha_1 gate (:162),
+ *                                        plus stage 1's q / k pooling (esa.py:107-111)
+ *   icsa_editing_sparse_attention_presummed
+ *                                   <- editing_sparse_attention (esa.py:67-232) fed by that
+ *                                        producer (q / k block sums already computed)
  */
 #ifndef ICSA_H_
 #define ICSA_H_
@@ -183,6 +190,52 @@ int icsa_gather_kv(const void* k, int k_dtype, int64_t k_sb, int64_t k_ss, int64
                    const void* v, int v_dtype, int64_t v_sb, int64_t v_ss, int64_t v_sh,
                    int B, int S, int H, int D, int t_seq_len, const int32_t* sel, int topK,
                    void* kn, void* vn, void* stream);
+
+/* Largest batch of icsa_wan_qk_prologue (per-batch RoPE grids travel as kernel arguments). */
+#define ICSA_WAN_MAX_BATCH 16
+
+/* Workspace bytes of icsa_wan_qk_prologue (two f32 [B, S] arrays of 1 / rms). */
+int64_t icsa_wan_qk_workspace_size(int B, int S);
+
+/* Producer of the attention inputs in the Wan DiT self-attention (model.py:156-171).
+ * yq, yk: the q / k projections [B, S, H*D] (bf16 or f32, both y_dtype; element strides
+ * y_sb, y_ss; each row contiguous).  For each token row: r = rsqrt(mean(y^2) + eps),
+ * n = bf16(y * r), m = n * w (wq / wk: f32 [H*D] RMSNorm weights), then the 3D RoPE of
+ * rope_apply: pair j of a head is rotated by rope_cos/sin[pos, j] (f32 [rope_rows, D/2],
+ * the model's freqs table), pos being the token's frame index for the first
+ * D/2 - 2*floor(D/6) pairs, its row and column index for floor(D/6) pairs each.  grids: host
+ * array int32 [B, 6] = target (f, h, w), source (f, h, w); target tokens come first, and
+ * with tag == 1 the source tokens follow on their own grid; later tokens are not rotated.
+ * Outputs: q_out / k_out bf16 [B, S, H, D] (strides o_*), qsum / ksum f32 [B*H, NB, D]
+ * 64-token block sums of the rotated f32 values (NB = ceil(S/64)), and, if alpha_logit
+ * is not NULL ([B, S] via al_sb, al_ss, the alpha_1(x) projection), gate_out f32 [B, S]
+ * = (sigmoid(a) - 0.5) * 0.5 computed with the reference's bf16 roundings.  B <= 16. */
+int icsa_wan_qk_prologue(
+    const void* yq, const void* yk, int y_dtype, int64_t y_sb, int64_t y_ss,
+    const float* wq, const float* wk, float eps,
+    const float* rope_cos, const float* rope_sin, int rope_rows,
+    const int32_t* grids, int tag,
+    const void* alpha_logit, int alpha_dtype, int64_t al_sb, int64_t al_ss,
+    int B, int S, int H, int D,
+    void* q_out, void* k_out, int64_t o_sb, int64_t o_ss, int64_t o_sh,
+    float* qsum, float* ksum, float* gate_out,
+    void* workspace, int64_t workspace_bytes, void* stream);
+
+/* icsa_editing_sparse_attention for q / k produced by icsa_wan_qk_prologue: q and k must
+ * be bf16, qsum / ksum are their f32 block sums [B*H, NB, D]; stage 1 then pools only v.
+ * Workspace: icsa_editing_workspace_size(..., ICSA_BF16, ICSA_BF16).  stage_events as in
+ * icsa_editing_sparse_attention_ev (NULL: none). */
+int icsa_editing_sparse_attention_presummed(
+    const void* q, int q_dtype, int64_t q_sb, int64_t q_ss, int64_t q_sh,
+    const void* k, int k_dtype, int64_t k_sb, int64_t k_ss, int64_t k_sh,
+    const void* v, int v_dtype, int64_t v_sb, int64_t v_ss, int64_t v_sh,
+    int B, int S, int H, int D, int t_seq_len, double sparsity, double srr, double flat_ratio,
+    const void* alpha, int alpha_dtype, int64_t a_sb, int64_t a_ss, int64_t a_sh, int64_t a_sd,
+    float alpha_scalar,
+    void* out, int out_dtype, int64_t o_sb, int64_t o_ss, int64_t o_sh,
+    const int32_t* inject_sel, const int32_t* inject_order, const int32_t* inject_l3,
+    void* workspace, int64_t workspace_bytes, void* stream, void* const* stage_events,
+    const float* qsum, const float* ksum);
 
 /* Last error message of the calling thread ("" if none). */
 const char* icsa_last_error(void);

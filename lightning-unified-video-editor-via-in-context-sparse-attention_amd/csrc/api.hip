@@ -197,7 +197,8 @@ namespace {
     a_sd, alpha_scalar, out, out_dtype, o_sb, o_ss, o_sh, inject_sel, inject_order,          \
     inject_l3, workspace, workspace_bytes, stream_
 
-int editing_impl(ICSA_EDITING_ARGS, void* const* stage_events) {
+int editing_impl(ICSA_EDITING_ARGS, void* const* stage_events, const float* qsum_in,
+                 const float* ksum_in) {
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
   auto mark = [&](int i) -> hipError_t {
     return stage_events ? hipEventRecord(reinterpret_cast<hipEvent_t>(stage_events[i]), stream)
@@ -209,6 +210,9 @@ int editing_impl(ICSA_EDITING_ARGS, void* const* stage_events) {
       (rc = check_dtype(v_dtype, "v")) || (rc = check_dtype(out_dtype, "out")))
     return rc;
   if (alpha && (rc = check_dtype(alpha_dtype, "alpha"))) return rc;
+  const bool presummed = qsum_in != nullptr || ksum_in != nullptr;
+  if (presummed && (!qsum_in || !ksum_in || q_dtype != ICSA_BF16 || k_dtype != ICSA_BF16))
+    return fail(ICSA_EINVAL, "presummed q/k: both qsum and ksum are required and q, k must be bf16");
   if (!q || !k || !v || !out || !workspace) return fail(ICSA_EINVAL, "null q/k/v/out/workspace pointer");
   if (!row_ok(q, q_dtype, q_sb, q_ss, q_sh) || !row_ok(k, k_dtype, k_sb, k_ss, k_sh) ||
       !row_ok(v, v_dtype, v_sb, v_ss, v_sh) || !row_ok(out, out_dtype, o_sb, o_ss, o_sh))
@@ -235,11 +239,13 @@ int editing_impl(ICSA_EDITING_ARGS, void* const* stage_events) {
   // ---- stage 1: pooling (+ V transposed, + bf16 copies of f32 q/k) ----
   PoolParams pp;
   std::memset(&pp, 0, sizeof(pp));
-  pp.x[0] = TokTensor{q, q_sb, q_ss, q_sh, q_dtype};
-  pp.x[1] = TokTensor{k, k_sb, k_ss, k_sh, k_dtype};
+  if (!presummed) {                 // q / k sums from their producer otherwise
+    pp.x[0] = TokTensor{q, q_sb, q_ss, q_sh, q_dtype};
+    pp.x[1] = TokTensor{k, k_sb, k_ss, k_sh, k_dtype};
+    pp.sums[0] = reinterpret_cast<float*>(WS(ICSA_WS_QSUM));
+    pp.sums[1] = reinterpret_cast<float*>(WS(ICSA_WS_KSUM));
+  }
   pp.x[2] = TokTensor{v, v_sb, v_ss, v_sh, v_dtype};
-  pp.sums[0] = reinterpret_cast<float*>(WS(ICSA_WS_QSUM));
-  pp.sums[1] = reinterpret_cast<float*>(WS(ICSA_WS_KSUM));
   pp.sums[2] = reinterpret_cast<float*>(WS(ICSA_WS_VSUM));
   pp.xb[0] = q_dtype == ICSA_F32 ? reinterpret_cast<bf16*>(WS(ICSA_WS_QB)) : nullptr;
   pp.xb[1] = k_dtype == ICSA_F32 ? reinterpret_cast<bf16*>(WS(ICSA_WS_KB)) : nullptr;
@@ -251,6 +257,8 @@ int editing_impl(ICSA_EDITING_ARGS, void* const* stage_events) {
   ICSA_HIP_TRY(mark(ICSA_STAGE_START), "event");
   ICSA_HIP_TRY(launch_pool(pp, stream), "pool");
   ICSA_HIP_TRY(mark(ICSA_STAGE_POOL), "event");
+  const float* qsum = presummed ? qsum_in : pp.sums[0];
+  const float* ksum = presummed ? ksum_in : pp.sums[1];
 
   // bf16 views of q / k used by the attention kernels
   const bf16* qb = q_dtype == ICSA_BF16 ? reinterpret_cast<const bf16*>(q) : pp.xb[0];
@@ -264,7 +272,7 @@ int editing_impl(ICSA_EDITING_ARGS, void* const* stage_events) {
 
   // ---- stage 2: compressed attention, retrieval, split ----
   CompressedParams cp;
-  cp.qsum = pp.sums[0]; cp.ksum = pp.sums[1]; cp.vsum = pp.sums[2];
+  cp.qsum = qsum; cp.ksum = ksum; cp.vsum = pp.sums[2];
   cp.P = reinterpret_cast<float*>(WS(ICSA_WS_P));
   cp.out_c = reinterpret_cast<float*>(WS(ICSA_WS_OUTC));
   cp.sharp = reinterpret_cast<float*>(WS(ICSA_WS_SHARP));
@@ -305,7 +313,7 @@ int editing_impl(ICSA_EDITING_ARGS, void* const* stage_events) {
   int64_t sk_vsb, sk_vsh, sk_vsd;
   int sk_Sk;
   if (!unaligned) {
-    np.ksum = pp.sums[1]; np.vsum = pp.sums[2];
+    np.ksum = ksum; np.vsum = pp.sums[2];
     np.kvmap = sp.kvmap; np.map_identity = 0; np.Nsrc = z.NB;
     sk_k = kb; sk_sb = kb_sb; sk_st = kb_ss; sk_sh = kb_sh;
     sk_vt = pp.vt; sk_vsb = pp.vt_sb; sk_vsh = pp.vt_sh; sk_vsd = pp.vt_sd;
@@ -348,7 +356,7 @@ int editing_impl(ICSA_EDITING_ARGS, void* const* stage_events) {
                                   hipMemcpyDeviceToDevice, stream), "inject l3");
     } else {
       Level3Params lp;
-      lp.qsum = pp.sums[0]; lp.rows = order; lp.rows_offset = z.n_peaked; lp.rows_stride = z.NB;
+      lp.qsum = qsum; lp.rows = order; lp.rows_offset = z.n_peaked; lp.rows_stride = z.NB;
       lp.kc32 = np.kc32; lp.idx = l3; lp.scores = reinterpret_cast<float*>(WS(ICSA_WS_L3S));
       lp.BH = BH; lp.NQsrc = z.NB; lp.n_rows = z.n_diffuse; lp.NKV = z.NKV; lp.top_k = z.top_k;
       ICSA_HIP_TRY(launch_level3(lp, stream), "level-3 top-k");
@@ -400,11 +408,85 @@ int editing_impl(ICSA_EDITING_ARGS, void* const* stage_events) {
 extern "C" {
 
 int icsa_editing_sparse_attention(ICSA_EDITING_ARGS) {
-  return editing_impl(ICSA_EDITING_PASS, nullptr);
+  return editing_impl(ICSA_EDITING_PASS, nullptr, nullptr, nullptr);
 }
 
 int icsa_editing_sparse_attention_ev(ICSA_EDITING_ARGS, void* const* stage_events) {
-  return editing_impl(ICSA_EDITING_PASS, stage_events);
+  return editing_impl(ICSA_EDITING_PASS, stage_events, nullptr, nullptr);
+}
+
+int icsa_editing_sparse_attention_presummed(ICSA_EDITING_ARGS, void* const* stage_events,
+                                            const float* qsum, const float* ksum) {
+  if (!qsum || !ksum) return fail(ICSA_EINVAL, "qsum / ksum are NULL");
+  return editing_impl(ICSA_EDITING_PASS, stage_events, qsum, ksum);
+}
+
+int64_t icsa_wan_qk_workspace_size(int B, int S) {
+  if (B <= 0 || S <= 0) return -1;
+  return align256((int64_t)B * S * 4) * 2;
+}
+
+int icsa_wan_qk_prologue(
+    const void* yq, const void* yk, int y_dtype, int64_t y_sb, int64_t y_ss,
+    const float* wq, const float* wk, float eps,
+    const float* rope_cos, const float* rope_sin, int rope_rows,
+    const int32_t* grids, int tag,
+    const void* alpha_logit, int alpha_dtype, int64_t al_sb, int64_t al_ss,
+    int B, int S, int H, int D,
+    void* q_out, void* k_out, int64_t o_sb, int64_t o_ss, int64_t o_sh,
+    float* qsum, float* ksum, float* gate_out,
+    void* workspace, int64_t workspace_bytes, void* stream_) {
+  int rc = validate_common(B, S, H, D);
+  if (rc) return rc;
+  if ((rc = check_dtype(y_dtype, "y"))) return rc;
+  if (alpha_logit && (rc = check_dtype(alpha_dtype, "alpha_logit"))) return rc;
+  if (B > ICSA_WAN_MAX_BATCH) return fail(ICSA_EUNSUPPORTED, "B=%d exceeds %d", B, ICSA_WAN_MAX_BATCH);
+  if (!yq || !yk || !wq || !wk || !rope_cos || !rope_sin || !grids || !q_out || !k_out || !qsum ||
+      !ksum || !workspace)
+    return fail(ICSA_EINVAL, "null pointer argument");
+  if (alpha_logit && !gate_out) return fail(ICSA_EINVAL, "alpha_logit given without gate_out");
+  if (!row_ok(yq, y_dtype, y_sb, y_ss, D) || !row_ok(yk, y_dtype, y_sb, y_ss, D) ||
+      !row_ok(q_out, ICSA_BF16, o_sb, o_ss, o_sh) || !row_ok(k_out, ICSA_BF16, o_sb, o_ss, o_sh))
+    return fail(ICSA_EINVAL, "y / q_out / k_out rows must be 16-byte aligned (pointer and strides)");
+  if (!aligned16(wq) || !aligned16(wk) || !aligned16(rope_cos) || !aligned16(rope_sin))
+    return fail(ICSA_EINVAL, "norm weights and RoPE tables must be 16-byte aligned");
+  if (!(eps >= 0.f)) return fail(ICSA_EINVAL, "eps must be >= 0");
+  if (tag != 0 && tag != 1) return fail(ICSA_EINVAL, "tag must be 0 or 1");
+  for (int b = 0; b < B; ++b)
+    for (int a = 0; a < 6; ++a) {
+      const int g = grids[6 * b + a];
+      if (g < 0 || (g > 0 && g > rope_rows))
+        return fail(ICSA_EINVAL, "grid size %d of batch %d outside [0, rope_rows=%d]", g, b, rope_rows);
+    }
+  const int64_t need = icsa_wan_qk_workspace_size(B, S);
+  if (workspace_bytes < need)
+    return fail(ICSA_EWORKSPACE, "workspace %lld bytes < required %lld", (long long)workspace_bytes,
+                (long long)need);
+  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+  char* ws = reinterpret_cast<char*>(workspace);
+  WanRmsParams rp;
+  std::memset(&rp, 0, sizeof(rp));
+  rp.y[0] = TokTensor{yq, y_sb, y_ss, D, y_dtype};
+  rp.y[1] = TokTensor{yk, y_sb, y_ss, D, y_dtype};
+  rp.rinv[0] = reinterpret_cast<float*>(ws);
+  rp.rinv[1] = reinterpret_cast<float*>(ws + align256((int64_t)B * S * 4));
+  rp.alpha_logit = TokTensor{alpha_logit, al_sb, al_ss, 0, alpha_dtype};
+  rp.gate = gate_out;
+  rp.B = B; rp.S = S; rp.H = H; rp.eps = eps;
+  WanQkParams qp;
+  std::memset(&qp, 0, sizeof(qp));
+  qp.y[0] = rp.y[0]; qp.y[1] = rp.y[1];
+  qp.w[0] = wq; qp.w[1] = wk;
+  qp.rinv[0] = rp.rinv[0]; qp.rinv[1] = rp.rinv[1];
+  qp.rope_cos = rope_cos; qp.rope_sin = rope_sin;
+  std::memcpy(qp.grids, grids, sizeof(int) * 6 * B);
+  qp.tag = tag;
+  qp.out[0] = OutView{q_out, o_sb, o_ss, o_sh, ICSA_DT_BF16};
+  qp.out[1] = OutView{k_out, o_sb, o_ss, o_sh, ICSA_DT_BF16};
+  qp.sums[0] = qsum; qp.sums[1] = ksum;
+  qp.B = B; qp.S = S; qp.H = H; qp.NB = ceil_div(S, ICSA_BLOCK);
+  ICSA_HIP_TRY(launch_wan_qk(rp, qp, stream), "wan q/k producer");
+  return ICSA_OK;
 }
 
 // ---------------------------------------------------------------------------------------

@@ -95,6 +95,30 @@ struct FlashParams {
 };
 hipError_t launch_flash(const FlashParams& p, hipStream_t stream);
 
+// ---------------------------------------------------------------- Wan q/k producer (wan_qk.hip)
+#define ICSA_WAN_MAX_B 16
+struct WanRmsParams {
+  TokTensor y[2];       // q / k projections [B, S, H*D] (sb, ss; rows contiguous)
+  float* rinv[2];       // [B, S] 1 / rms of each row
+  TokTensor alpha_logit;   // [B, S] alpha_1(x) (p == nullptr -> no gate)
+  float* gate;          // [B, S] (sigmoid(a) - 0.5) * 0.5 in the reference's bf16 steps
+  int B, S, H;
+  float eps;
+};
+struct WanQkParams {
+  TokTensor y[2];       // as WanRmsParams::y (same dtype)
+  const float* w[2];    // RMSNorm weights [H*D]
+  const float* rinv[2]; // WanRmsParams::rinv
+  const float* rope_cos;   // [rope_rows, D/2]  cos / sin of the model's freqs table
+  const float* rope_sin;
+  int grids[6 * ICSA_WAN_MAX_B];   // per batch: target f, h, w; source f, h, w
+  int tag;              // 1: source tokens rotated on their own grid after the target
+  OutView out[2];       // bf16 [B, S, H, D]
+  float* sums[2];       // [B, H, NB, D] fp32 block sums of the rotated fp32 values
+  int B, S, H, NB;
+};
+hipError_t launch_wan_qk(const WanRmsParams& rp, const WanQkParams& qp, hipStream_t stream);
+
 // ---------------------------------------------------------------- stage 4 (sparse_attn.hip)
 struct SparseParams {
   const bf16* q; int64_t q_sb, q_ss, q_sh;      // [B, Sq, H, D]

@@ -39,7 +39,8 @@ EXPORTS = [
     "icsa_editing_sparse_attention", "icsa_editing_sparse_attention_ev",
     "icsa_sparse_piecewise_workspace_size",
     "icsa_sparse_piecewise_attn", "icsa_flash_attn_workspace_size", "icsa_flash_attn",
-    "icsa_pool", "icsa_gather_kv", "icsa_last_error", "icsa_version",
+    "icsa_pool", "icsa_gather_kv", "icsa_wan_qk_workspace_size", "icsa_wan_qk_prologue",
+    "icsa_editing_sparse_attention_presummed", "icsa_last_error", "icsa_version",
 ]
 
 _p = ctypes.c_void_p
@@ -96,6 +97,27 @@ _SIGNATURES = {
         _p, _i, _l, _l, _l,
         _p, _i, _l, _l, _l,
         _i, _i, _i, _i, _i, _p, _i, _p, _p, _p]),
+    "icsa_wan_qk_workspace_size": (_l, [_i, _i]),
+    "icsa_wan_qk_prologue": (_i, [
+        _p, _p, _i, _l, _l,
+        _p, _p, _f,
+        _p, _p, _i,
+        _p, _i,
+        _p, _i, _l, _l,
+        _i, _i, _i, _i,
+        _p, _p, _l, _l, _l,
+        _p, _p, _p,
+        _p, _l, _p]),
+    "icsa_editing_sparse_attention_presummed": (_i, [
+        _p, _i, _l, _l, _l,
+        _p, _i, _l, _l, _l,
+        _p, _i, _l, _l, _l,
+        _i, _i, _i, _i, _i, _d, _d, _d,
+        _p, _i, _l, _l, _l, _l, _f,
+        _p, _i, _l, _l, _l,
+        _p, _p, _p,
+        _p, _l, _p, _p,
+        _p, _p]),
     "icsa_last_error": (ctypes.c_char_p, []),
     "icsa_version": (_i, []),
 }

@@ -65,11 +65,14 @@ def _alpha_view(alpha_2, B, S, H, D, device):
 @torch.no_grad()
 def _editing_sparse_attention_hip(q, k, v, t_seq_len, alpha_2=1.0, SPARSITY_RATIO=0.0625,
                                   srr=0.125, flat_ratio=0.5, inject=None, keep_workspace=False,
-                                  stage_events=None):
+                                  stage_events=None, presummed=None, out_dtype=None):
     """Runs the fused HIP path; returns ``(x, workspace_views or None)``.
 
     ``stage_events``: optional list of ``len(_lib.STAGES)`` recorded ``torch.cuda.Event``s
     (enable_timing=True) that the library re-records at each stage boundary on the stream.
+    ``presummed``: optional ``(qsum, ksum)`` f32 [B, H, NB, D] block sums of bf16 q / k from
+    their producer (``wan.wan_qk_prologue``); stage 1 then pools only v.
+    ``out_dtype``: dtype of x (default q.dtype, as the reference).
     """
     _require(q.is_cuda and k.is_cuda and v.is_cuda, "q, k, v must be on the GPU")
     _require(q.ndim == 4 and q.shape == k.shape == v.shape, "q, k, v must be [B, S, H, D]")
@@ -87,7 +90,16 @@ def _editing_sparse_attention_hip(q, k, v, t_seq_len, alpha_2=1.0, SPARSITY_RATI
     if ws_bytes < 0:
         raise _lib.IcsaError("icsa_editing_workspace_layout", int(ws_bytes))
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
-    out = torch.empty(B, S, H, D, dtype=q.dtype, device=q.device)
+    out = torch.empty(B, S, H, D, dtype=out_dtype or q.dtype, device=q.device)
+    sums_args = []
+    if presummed is not None:
+        qsum, ksum = presummed
+        NB = sizes["NB"]
+        for name, t in (("qsum", qsum), ("ksum", ksum)):
+            _require(t.is_cuda and t.dtype == torch.float32 and t.is_contiguous()
+                     and tuple(t.shape) == (B, H, NB, D), f"{name} must be contiguous f32 {(B, H, NB, D)}")
+        _require(q.dtype == torch.bfloat16 and k.dtype == torch.bfloat16,
+                 "presummed q / k must be bfloat16")
     a, a_scalar, a_dt, a_st = _alpha_view(alpha_2, B, S, H, D, q.device)
     inject = inject or {}
     inj = {}
@@ -104,6 +116,9 @@ def _editing_sparse_attention_hip(q, k, v, t_seq_len, alpha_2=1.0, SPARSITY_RATI
         handles = (ctypes.c_void_p * len(stage_events))(*[e.cuda_event for e in stage_events])
         ev_args = [ctypes.cast(handles, ctypes.c_void_p)]
         fn = L.icsa_editing_sparse_attention_ev
+    if presummed is not None:
+        fn = L.icsa_editing_sparse_attention_presummed
+        ev_args = (ev_args or [None]) + [ptr(presummed[0]), ptr(presummed[1])]
     rc = fn(
         ptr(q), dtype_code(q), q.stride(0), q.stride(1), q.stride(2),
         ptr(k), dtype_code(k), k.stride(0), k.stride(1), k.stride(2),
