@@ -201,6 +201,123 @@ def wan_attention_bench(steps, warmup, log_fn):
     return res
 
 
+def block_bench(steps, warmup, log_fn):
+    """Configuration 4: one Wan 2.2 14B DiT block forward (dim 5120, 40 heads, FFN 13,824,
+    cross_attn_norm) over 65,520 tokens (21x30x52 target + source grids), cross attention to
+    512 text tokens, bf16 random-init weights (the reference's init_weights scheme), adaLN
+    time embedding of t ~ U(0, 1000).  Timed: (a) the HIP block
+    (in_context_sparse_attention.wan.WanAttentionBlock); (b) the same parameters through the
+    reference's PyTorch glue (LayerNorm / modulation / residual in fp32, WanRMSNorm, float64
+    RoPE, fp32 q / k into the attention path), with the same attention kernels."""
+    import math as _m
+    import torch
+    import torch.nn as nn
+    import torch.nn.functional as F
+    from in_context_sparse_attention import editing_sparse_attention, flash_attn_func, wan
+    dev = torch.device("cuda:0")
+    dim, H, ffn, L, text_dim, freq_dim = 5120, 40, 13824, 512, 4096, 256
+    D = dim // H
+    grid = (21, 30, 52)
+    S = 2 * grid[0] * grid[1] * grid[2]
+    t_len = S // 2
+    torch.manual_seed(0)
+    blk = wan.WanAttentionBlock("t2v_cross_attn", dim, ffn, H, cross_attn_norm=True)
+    for m in blk.modules():                       # WanModel.init_weights (model.py:387-397)
+        if isinstance(m, nn.Linear):
+            nn.init.xavier_uniform_(m.weight)
+            if m.bias is not None:
+                nn.init.zeros_(m.bias)
+    blk = blk.to(dev).to(torch.bfloat16)
+    with torch.no_grad():
+        # adaLN input: sinusoidal embedding of t -> time_embedding -> time_projection (model.py:433-436)
+        tstep = torch.rand(1) * 1000
+        half = freq_dim // 2
+        sinus = torch.outer(tstep.double(), torch.pow(10000, -torch.arange(half).double().div(half)))
+        emb = torch.cat([torch.cos(sinus), torch.sin(sinus)], dim=1).float().to(dev)
+        te = nn.Sequential(nn.Linear(freq_dim, dim), nn.SiLU(), nn.Linear(dim, dim)).to(dev)
+        tp = nn.Sequential(nn.SiLU(), nn.Linear(dim, dim * 6)).to(dev)
+        for m in te.modules():
+            if isinstance(m, nn.Linear):
+                nn.init.normal_(m.weight, std=0.02)
+        e0 = tp(te(emb)).unflatten(1, (6, dim)).float()
+        # 512 text tokens of dim 4096 -> text_embedding (model.py:360-361, 438-439)
+        txt = nn.Sequential(nn.Linear(text_dim, dim), nn.GELU(approximate="tanh"),
+                            nn.Linear(dim, dim)).to(dev)
+        for m in txt.modules():
+            if isinstance(m, nn.Linear):
+                nn.init.normal_(m.weight, std=0.02)
+        ctx = txt(torch.randn(1, L, text_dim, device=dev)).to(torch.bfloat16)
+        x = torch.randn(1, S, dim, device=dev)
+        freqs = wan.wan_freqs(D)
+        seq_lens = torch.tensor([S])
+
+        def hip_block():
+            return blk(x, e0, seq_lens, [grid], freqs, ctx, None, [grid], 1)
+
+        sa, ca = blk.self_attn, blk.cross_attn
+
+        def rms(y, w, eps=1e-6):
+            z = y.float()
+            return (z * torch.rsqrt(z.pow(2).mean(-1, keepdim=True) + eps)).type_as(y) * w
+
+        def ref_block():
+            em = (blk.modulation.float() + e0).chunk(6, dim=1)
+            h = F.layer_norm(x.float(), (dim,), eps=1e-6).float() * (1 + em[1]) + em[0]
+            hb = h.to(torch.bfloat16)
+            q, k, g = reference_glue(sa.q(hb), sa.k(hb), sa.alpha_1(hb), sa.norm_q.weight.float(),
+                                     sa.norm_k.weight.float(), grid, freqs, H)
+            a = editing_sparse_attention(q, k, sa.v(hb).view(1, S, H, D), t_len, S - t_len,
+                                         alpha_2=g, backend="hip")
+            y = sa.o(a.flatten(2).to(torch.bfloat16))
+            xr = x + y * em[2]
+            n3 = F.layer_norm(xr, (dim,), blk.norm3.weight.float(), blk.norm3.bias.float(), 1e-6)
+            n3b = n3.to(torch.bfloat16)
+            cq = rms(ca.q(n3b), ca.norm_q.weight.float()).view(1, S, H, D).to(torch.bfloat16)
+            ck = rms(ca.k(ctx), ca.norm_k.weight.float()).view(1, L, H, D).to(torch.bfloat16)
+            cv = ca.v(ctx).view(1, L, H, D)
+            xr = xr + ca.o(flash_attn_func(cq, ck, cv).flatten(2))
+            h = F.layer_norm(xr, (dim,), eps=1e-6) * (1 + em[4]) + em[3]
+            y = blk.ffn(h.to(torch.bfloat16))
+            return xr + y * em[5]
+
+        stream = torch.cuda.current_stream(dev)
+
+        def timed(fn, n):
+            ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                  for _ in range(n)]
+            for a_, b_ in ev:
+                a_.record(stream)
+                fn()
+                b_.record(stream)
+            torch.cuda.synchronize()
+            return statistics.mean(a_.elapsed_time(b_) for a_, b_ in ev)
+
+        for fn in (hip_block, ref_block):
+            for _ in range(max(1, warmup)):
+                fn()
+        torch.cuda.synchronize()
+        n = max(3, steps // 4)
+        hip_ms = timed(hip_block, n)
+        ref_ms = timed(ref_block, n)
+        # GEMM work of the block (2 flops per multiply-add)
+        # self q, k, v, o and cross q, o on the S tokens; cross k, v on the L text tokens;
+        # FFN up / down; the alpha_1 projection
+        gemm_flops = (2.0 * S * dim * dim * 6 + 2.0 * L * dim * dim * 2 + 2.0 * S * dim * ffn * 2
+                      + 2.0 * S * dim)
+        attn_flops = 4.0 * S * L * dim
+    res = {"block_ms": hip_ms, "reference_glue_block_ms": ref_ms,
+           "speedup_vs_reference_glue": ref_ms / hip_ms,
+           "gemm_tflop": gemm_flops / 1e12, "cross_attn_tflop": attn_flops / 1e12,
+           "workload": (f"configuration 4: one DiT block, dim {dim}, {H} heads, FFN {ffn}, S={S} "
+                        f"(grids {grid} + {grid}), {L} text tokens, bf16 random-init weights, "
+                        f"t={float(tstep):.1f}")}
+    log_fn(f"[bench] DiT block (cfg 4): HIP {hip_ms:.2f} ms; reference glue around the same "
+           f"attention kernels {ref_ms:.2f} ms")
+    del blk
+    torch.cuda.empty_cache()
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -219,6 +336,10 @@ def main():
                          "reference's glue)")
     ap.add_argument("--wan-only", action="store_true",
                     help="run only the configuration-4 WanSelfAttention leg (for profiling)")
+    ap.add_argument("--no-block", action="store_true",
+                    help="skip the configuration-4 DiT block leg")
+    ap.add_argument("--block-only", action="store_true",
+                    help="run only the configuration-4 DiT block leg (for profiling)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
                     help="after the timed steps, run 3 elementwise copies (torch.neg) of BYTES "
                          "bytes: the reference kernel of known traffic that scales the HBM "
@@ -240,6 +361,9 @@ def main():
     _lib.lib()
     if args.wan_only:
         print(json.dumps({"wan_attention": wan_attention_bench(args.steps, args.warmup, log)}), flush=True)
+        return
+    if args.block_only:
+        print(json.dumps({"dit_block": block_bench(args.steps, args.warmup, log)}), flush=True)
         return
     q, k, v, t = config_inputs(args.config, device=dev)
     B, S, H, D = q.shape
@@ -369,6 +493,8 @@ def main():
         del q, k, v
         torch.cuda.empty_cache()
         result["wan_attention"] = wan_attention_bench(args.steps, args.warmup, log)
+    if not args.no_block:
+        result["dit_block"] = block_bench(args.steps, args.warmup, log)
     if not args.no_cpu_baseline:
         cb = cpu_baseline(args.cpu_seconds)
         log(f"[bench] cpu baseline: {cb['sample']} on {cb['cores']} threads")

@@ -34,6 +34,9 @@
  *                                        model.py:156-171: WanRMSNorm (model.py:103-114),
  *                                        rope_apply (model.py:69-95), alpha_1 gate (:162),
  *                                        plus stage 1's q / k pooling (esa.py:107-111)
+ *   icsa_wan_ln_modulate            <- the residual / LayerNorm / adaLN steps of
+ *                                        WanAttentionBlock.forward, model.py:249-270
+ *                                        (WanLayerNorm, model.py:117-122)
  *   icsa_editing_sparse_attention_presummed
  *                                   <- editing_sparse_attention (esa.py:67-232) fed by that
  *                                        producer (q / k block sums already computed)
@@ -209,7 +212,10 @@ int64_t icsa_wan_qk_workspace_size(int B, int S);
  * Outputs: q_out / k_out bf16 [B, S, H, D] (strides o_*), qsum / ksum f32 [B*H, NB, D]
  * 64-token block sums of the rotated f32 values (NB = ceil(S/64)), and, if alpha_logit
  * is not NULL ([B, S] via al_sb, al_ss, the alpha_1(x) projection), gate_out f32 [B, S]
- * = (sigmoid(a) - 0.5) * 0.5 computed with the reference's bf16 roundings.  B <= 16. */
+ * = (sigmoid(a) - 0.5) * 0.5 computed with the reference's bf16 roundings.  B <= 16.
+ * Single-tensor mode: yk == NULL processes q only (wk, k_out, ksum ignored); qsum == NULL
+ * (with ksum NULL) skips the block sums.  With every grid extent 0 nothing is rotated:
+ * the q / k RMSNorm of the cross attention (model.py:180-188). */
 int icsa_wan_qk_prologue(
     const void* yq, const void* yk, int y_dtype, int64_t y_sb, int64_t y_ss,
     const float* wq, const float* wk, float eps,
@@ -236,6 +242,22 @@ int icsa_editing_sparse_attention_presummed(
     const int32_t* inject_sel, const int32_t* inject_order, const int32_t* inject_l3,
     void* workspace, int64_t workspace_bytes, void* stream, void* const* stage_events,
     const float* qsum, const float* ksum);
+
+/* One pass of the Wan DiT block glue per token row (model.py:249-270):
+ *   x' = x + y * gate             if y != NULL (y bf16 [B, S, dim], gate f32 [B, dim] by g_sb;
+ *                                  x' written to x_out f32 [B, S, dim], which may alias x)
+ *   out = bf16( LN(x') [* lw + lb] [* (1 + scale) + shift] )   if out != NULL
+ * LN: LayerNorm over dim without affine (WanLayerNorm), eps; lw / lb: optional f32 [dim]
+ * affine (norm3); shift / scale: optional f32 [B, dim] by mod_sb (adaLN e[0] / e[1] and
+ * e[3] / e[4]).  x: bf16 or f32 [B, S, dim] (strides x_sb, x_ss); for bf16 x the LayerNorm
+ * result is rounded to bf16 first (.type_as(x)).  dim % 4 == 0, dim <= 6144; rows 16-byte
+ * aligned. */
+int icsa_wan_ln_modulate(const void* x, int x_dtype, int64_t x_sb, int64_t x_ss,
+                         const void* y, int64_t y_sb, int64_t y_ss, const float* gate, int64_t g_sb,
+                         float* x_out, int64_t xo_sb, int64_t xo_ss,
+                         const float* lw, const float* lb,
+                         const float* shift, const float* scale, int64_t mod_sb, float eps,
+                         int B, int S, int dim, void* out, int64_t o_sb, int64_t o_ss, void* stream);
 
 /* Last error message of the calling thread ("" if none). */
 const char* icsa_last_error(void);

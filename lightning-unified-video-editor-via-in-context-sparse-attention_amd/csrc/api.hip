@@ -421,6 +421,41 @@ int icsa_editing_sparse_attention_presummed(ICSA_EDITING_ARGS, void* const* stag
   return editing_impl(ICSA_EDITING_PASS, stage_events, qsum, ksum);
 }
 
+int icsa_wan_ln_modulate(const void* x, int x_dtype, int64_t x_sb, int64_t x_ss,
+                         const void* y, int64_t y_sb, int64_t y_ss, const float* gate, int64_t g_sb,
+                         float* x_out, int64_t xo_sb, int64_t xo_ss,
+                         const float* lw, const float* lb,
+                         const float* shift, const float* scale, int64_t mod_sb, float eps,
+                         int B, int S, int dim, void* out, int64_t o_sb, int64_t o_ss, void* stream_) {
+  int rc = check_dtype(x_dtype, "x");
+  if (rc) return rc;
+  if (B <= 0 || S <= 0 || dim <= 0) return fail(ICSA_EINVAL, "B, S, dim must be positive");
+  if (dim % 4 != 0 || dim > 6144) return fail(ICSA_EUNSUPPORTED, "dim=%d: need dim %% 4 == 0 and <= 6144", dim);
+  if (!x) return fail(ICSA_EINVAL, "x is NULL");
+  if (y && (!gate || !x_out)) return fail(ICSA_EINVAL, "y given without gate / x_out");
+  if (!y && !out) return fail(ICSA_EINVAL, "nothing to do (y and out are NULL)");
+  if (!lw != !lb) return fail(ICSA_EINVAL, "lw and lb must be both given or both NULL");
+  if (!shift != !scale) return fail(ICSA_EINVAL, "shift and scale must be both given or both NULL");
+  auto al = [&](const void* p, int64_t s0, int64_t s1, int es) {
+    return p == nullptr || (aligned16(p) && (s0 * es) % 16 == 0 && (s1 * es) % 16 == 0);
+  };
+  if (!al(x, x_sb, x_ss, elsize(x_dtype)) || !al(y, y_sb, y_ss, 2) || !al(gate, g_sb, 0, 4) ||
+      !al(x_out, xo_sb, xo_ss, 4) || !al(lw, 0, 0, 4) || !al(lb, 0, 0, 4) || !al(shift, mod_sb, 0, 4) ||
+      !al(scale, mod_sb, 0, 4) || !al(out, o_sb, o_ss, 2) || (dim * 2) % 16 != 0)
+    return fail(ICSA_EINVAL, "rows must be 16-byte aligned (pointers and strides)");
+  LnModParams p;
+  std::memset(&p, 0, sizeof(p));
+  p.x = x; p.x_dtype = x_dtype; p.x_sb = x_sb; p.x_ss = x_ss;
+  p.y = reinterpret_cast<const bf16*>(y); p.y_sb = y_sb; p.y_ss = y_ss;
+  p.gate = gate; p.g_sb = g_sb;
+  p.x_out = x_out; p.xo_sb = xo_sb; p.xo_ss = xo_ss;
+  p.lw = lw; p.lb = lb; p.shift = shift; p.scale = scale; p.mod_sb = mod_sb;
+  p.out = reinterpret_cast<bf16*>(out); p.o_sb = o_sb; p.o_ss = o_ss;
+  p.B = B; p.S = S; p.dim = dim; p.eps = eps;
+  ICSA_HIP_TRY(launch_ln_mod(p, reinterpret_cast<hipStream_t>(stream_)), "layer norm / modulate");
+  return ICSA_OK;
+}
+
 int64_t icsa_wan_qk_workspace_size(int B, int S) {
   if (B <= 0 || S <= 0) return -1;
   return align256((int64_t)B * S * 4) * 2;
@@ -441,14 +476,15 @@ int icsa_wan_qk_prologue(
   if ((rc = check_dtype(y_dtype, "y"))) return rc;
   if (alpha_logit && (rc = check_dtype(alpha_dtype, "alpha_logit"))) return rc;
   if (B > ICSA_WAN_MAX_BATCH) return fail(ICSA_EUNSUPPORTED, "B=%d exceeds %d", B, ICSA_WAN_MAX_BATCH);
-  if (!yq || !yk || !wq || !wk || !rope_cos || !rope_sin || !grids || !q_out || !k_out || !qsum ||
-      !ksum || !workspace)
+  if (!yq || !wq || !rope_cos || !rope_sin || !grids || !q_out || !workspace)
     return fail(ICSA_EINVAL, "null pointer argument");
+  if (yk && (!wk || !k_out)) return fail(ICSA_EINVAL, "yk given without wk / k_out");
+  if (!qsum != !(yk ? ksum : qsum)) return fail(ICSA_EINVAL, "qsum and ksum must be both given or both NULL");
   if (alpha_logit && !gate_out) return fail(ICSA_EINVAL, "alpha_logit given without gate_out");
-  if (!row_ok(yq, y_dtype, y_sb, y_ss, D) || !row_ok(yk, y_dtype, y_sb, y_ss, D) ||
-      !row_ok(q_out, ICSA_BF16, o_sb, o_ss, o_sh) || !row_ok(k_out, ICSA_BF16, o_sb, o_ss, o_sh))
+  if (!row_ok(yq, y_dtype, y_sb, y_ss, D) || (yk && !row_ok(yk, y_dtype, y_sb, y_ss, D)) ||
+      !row_ok(q_out, ICSA_BF16, o_sb, o_ss, o_sh) || (yk && !row_ok(k_out, ICSA_BF16, o_sb, o_ss, o_sh)))
     return fail(ICSA_EINVAL, "y / q_out / k_out rows must be 16-byte aligned (pointer and strides)");
-  if (!aligned16(wq) || !aligned16(wk) || !aligned16(rope_cos) || !aligned16(rope_sin))
+  if (!aligned16(wq) || (yk && !aligned16(wk)) || !aligned16(rope_cos) || !aligned16(rope_sin))
     return fail(ICSA_EINVAL, "norm weights and RoPE tables must be 16-byte aligned");
   if (!(eps >= 0.f)) return fail(ICSA_EINVAL, "eps must be >= 0");
   if (tag != 0 && tag != 1) return fail(ICSA_EINVAL, "tag must be 0 or 1");
@@ -467,7 +503,7 @@ int icsa_wan_qk_prologue(
   WanRmsParams rp;
   std::memset(&rp, 0, sizeof(rp));
   rp.y[0] = TokTensor{yq, y_sb, y_ss, D, y_dtype};
-  rp.y[1] = TokTensor{yk, y_sb, y_ss, D, y_dtype};
+  rp.y[1] = TokTensor{yk, y_sb, y_ss, D, y_dtype};      // p == nullptr: q only
   rp.rinv[0] = reinterpret_cast<float*>(ws);
   rp.rinv[1] = reinterpret_cast<float*>(ws + align256((int64_t)B * S * 4));
   rp.alpha_logit = TokTensor{alpha_logit, al_sb, al_ss, 0, alpha_dtype};

@@ -119,6 +119,20 @@ struct WanQkParams {
 };
 hipError_t launch_wan_qk(const WanRmsParams& rp, const WanQkParams& qp, hipStream_t stream);
 
+// ---------------------------------------------------------------- Wan block glue (wan_block.hip)
+struct LnModParams {
+  const void* x; int x_dtype; int64_t x_sb, x_ss;      // residual stream [B, S, dim]
+  const bf16* y; int64_t y_sb, y_ss;                    // optional update x += y * gate
+  const float* gate; int64_t g_sb;                      // [B, dim]
+  float* x_out; int64_t xo_sb, xo_ss;                   // updated x (f32; may alias x)
+  const float* lw; const float* lb;                     // optional LayerNorm affine [dim]
+  const float* shift; const float* scale; int64_t mod_sb;   // optional [B, dim] modulation
+  bf16* out; int64_t o_sb, o_ss;                        // bf16 [B, S, dim] (nullptr: update only)
+  int B, S, dim;
+  float eps;
+};
+hipError_t launch_ln_mod(const LnModParams& p, hipStream_t stream);
+
 // ---------------------------------------------------------------- stage 4 (sparse_attn.hip)
 struct SparseParams {
   const bf16* q; int64_t q_sb, q_ss, q_sh;      // [B, Sq, H, D]

@@ -33,6 +33,7 @@ __global__ void __launch_bounds__(256) icsa_wan_rms_kernel(WanRmsParams p) {
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const TokTensor& y = p.y[i];
+    if (y.p == nullptr) continue;           // single-tensor mode (k absent)
     float ss = 0.f;
     for (int c = lane; c < dim / 8; c += 64) {
       float v[8];
@@ -101,15 +102,17 @@ __global__ void __launch_bounds__(256) icsa_wan_qk_kernel(WanQkParams p) {
   } else if (t < 3 * ICSA_BLOCK) {          // 1 / rms of the block's q and k rows
     const int i = (t - ICSA_BLOCK) / ICSA_BLOCK, r = t % ICSA_BLOCK;
     const int tok = n * ICSA_BLOCK + r;
-    r_s[i][r] = tok < p.S ? p.rinv[i][(int64_t)b * p.S + tok] : 0.f;
+    r_s[i][r] = (tok < p.S && p.y[i].p != nullptr) ? p.rinv[i][(int64_t)b * p.S + tok] : 0.f;
   }
   __syncthreads();
   const int c = t & 15;          // chunk of 8 dims: pairs 4c .. 4c + 3
   const int g = t >> 4;          // 16 token groups of 4 tokens
+  const int nt = p.y[1].p != nullptr ? 2 : 1;     // single-tensor mode: q only
   const T* ybase[2];
   float w[2][8];
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
+    if (i >= nt) break;
     ybase[i] = reinterpret_cast<const T*>(p.y[i].p) + (int64_t)b * p.y[i].sb + (int64_t)h * ICSA_D + 8 * c;
     load8_f32<float>(p.w[i] + h * ICSA_D + 8 * c, w[i]);
   }
@@ -134,7 +137,8 @@ __global__ void __launch_bounds__(256) icsa_wan_qk_kernel(WanQkParams p) {
     if (tok >= p.S) continue;
     float v[2][8];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) load8_f32<T>(ybase[i] + (int64_t)tok * p.y[i].ss, v[i]);
+    for (int i = 0; i < 2; ++i)
+      if (i < nt) load8_f32<T>(ybase[i] + (int64_t)tok * p.y[i].ss, v[i]);
     const int* pos = pos_s[r];
     float cs[4], sn[4];
     if (one_axis) {                        // the chunk's 4 pairs use one axis: one row segment
@@ -158,6 +162,7 @@ __global__ void __launch_bounds__(256) icsa_wan_qk_kernel(WanQkParams p) {
     }
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
+      if (i >= nt) break;
       const float rr = r_s[i][r];
       float m[8];
 #pragma unroll
@@ -188,10 +193,12 @@ __global__ void __launch_bounds__(256) icsa_wan_qk_kernel(WanQkParams p) {
   __syncthreads();
   {
     const int i = t >> 7, d = t & 127;     // 256 threads: (tensor, dim)
-    float s = 0.f;
+    if (i < nt && p.sums[i] != nullptr) {
+      float s = 0.f;
 #pragma unroll
-    for (int gg = 0; gg < 16; ++gg) s += red[i][gg][d];      // fixed order, as the pool kernel
-    p.sums[i][(((int64_t)b * p.H + h) * p.NB + n) * ICSA_D + d] = s;
+      for (int gg = 0; gg < 16; ++gg) s += red[i][gg][d];    // fixed order, as the pool kernel
+      p.sums[i][(((int64_t)b * p.H + h) * p.NB + n) * ICSA_D + d] = s;
+    }
   }
 }
 

@@ -40,7 +40,8 @@ EXPORTS = [
     "icsa_sparse_piecewise_workspace_size",
     "icsa_sparse_piecewise_attn", "icsa_flash_attn_workspace_size", "icsa_flash_attn",
     "icsa_pool", "icsa_gather_kv", "icsa_wan_qk_workspace_size", "icsa_wan_qk_prologue",
-    "icsa_editing_sparse_attention_presummed", "icsa_last_error", "icsa_version",
+    "icsa_editing_sparse_attention_presummed", "icsa_wan_ln_modulate", "icsa_last_error",
+    "icsa_version",
 ]
 
 _p = ctypes.c_void_p
@@ -118,6 +119,13 @@ _SIGNATURES = {
         _p, _p, _p,
         _p, _l, _p, _p,
         _p, _p]),
+    "icsa_wan_ln_modulate": (_i, [
+        _p, _i, _l, _l,
+        _p, _l, _l, _p, _l,
+        _p, _l, _l,
+        _p, _p,
+        _p, _p, _l, _f,
+        _i, _i, _i, _p, _l, _l, _p]),
     "icsa_last_error": (ctypes.c_char_p, []),
     "icsa_version": (_i, []),
 }

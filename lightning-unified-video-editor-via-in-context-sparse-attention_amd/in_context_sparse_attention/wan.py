@@ -54,10 +54,11 @@ def rope_tables(freqs: torch.Tensor, device) -> tuple[torch.Tensor, torch.Tensor
     if hit is None:
         f = freqs.to(torch.complex128)
         hit = (f.real.to(device=device, dtype=torch.float32).contiguous(),
-               f.imag.to(device=device, dtype=torch.float32).contiguous())
-        _rope_cache.clear()
-        _rope_cache[key] = hit
-    return hit
+               f.imag.to(device=device, dtype=torch.float32).contiguous(), freqs)
+        if len(_rope_cache) >= 8:                    # a few live tables (model, identity)
+            _rope_cache.pop(next(iter(_rope_cache)))
+        _rope_cache[key] = hit                       # keeps freqs alive: its address stays unique
+    return hit[0], hit[1]
 
 
 def _grids(grid_sizes, source_video_grid_sizes, B) -> ctypes.Array:
@@ -73,37 +74,44 @@ def _grids(grid_sizes, source_video_grid_sizes, B) -> ctypes.Array:
 
 
 @torch.no_grad()
-def wan_qk_prologue(yq: torch.Tensor, yk: torch.Tensor, norm_q_weight: torch.Tensor,
-                    norm_k_weight: torch.Tensor, grid_sizes, source_video_grid_sizes, TAG: int,
-                    freqs: torch.Tensor, num_heads: int, alpha_logit: torch.Tensor = None,
-                    eps: float = 1e-6):
+def wan_qk_prologue(yq: torch.Tensor, yk, norm_q_weight: torch.Tensor, norm_k_weight,
+                    grid_sizes, source_video_grid_sizes, TAG: int, freqs: torch.Tensor,
+                    num_heads: int, alpha_logit: torch.Tensor = None, eps: float = 1e-6,
+                    want_sums: bool = True):
     """q / k producer of WanSelfAttention.forward on the q / k projections yq, yk [B, S, dim].
 
     Returns ``(q, k, qsum, ksum, gate)``: bf16 q, k [B, S, H, D]; f32 block sums
-    [B, H, NB, D]; f32 gate [B, S] (None without ``alpha_logit``)."""
-    _require(yq.is_cuda and yk.is_cuda, "yq, yk must be on the GPU")
-    _require(yq.dim() == 3 and yq.shape == yk.shape, "yq, yk must be [B, S, dim]")
-    _require(yq.dtype == yk.dtype, "yq and yk must have the same dtype")
+    [B, H, NB, D] (None without ``want_sums``); f32 gate [B, S] (None without
+    ``alpha_logit``).  ``yk=None`` processes q alone (k, ksum None); all-zero grids rotate
+    nothing (the cross attention's RMSNorm)."""
+    _require(yq.is_cuda and yq.dim() == 3, "yq must be [B, S, dim] on the GPU")
+    if yk is not None:
+        _require(yk.is_cuda and yq.shape == yk.shape and yq.dtype == yk.dtype,
+                 "yk must match yq in shape and dtype")
     B, S, dim = yq.shape
     H = int(num_heads)
     _require(dim % H == 0, "dim must be a multiple of num_heads")
     D = dim // H
     yq = yq if yq.stride(-1) == 1 else yq.contiguous()
-    yk = yk if yk.stride(-1) == 1 else yk.contiguous()
-    if yk.stride() != yq.stride():
-        yq, yk = yq.contiguous(), yk.contiguous()
+    if yk is not None:
+        yk = yk if yk.stride(-1) == 1 else yk.contiguous()
+        if yk.stride() != yq.stride():
+            yq, yk = yq.contiguous(), yk.contiguous()
     dev = yq.device
     wq = norm_q_weight.detach().to(device=dev, dtype=torch.float32).contiguous()
-    wk = norm_k_weight.detach().to(device=dev, dtype=torch.float32).contiguous()
-    _require(wq.numel() == dim and wk.numel() == dim, "norm weights must have dim elements")
+    _require(wq.numel() == dim, "norm weights must have dim elements")
+    wk = None
+    if yk is not None:
+        wk = norm_k_weight.detach().to(device=dev, dtype=torch.float32).contiguous()
+        _require(wk.numel() == dim, "norm weights must have dim elements")
     cos, sin = rope_tables(freqs, dev)
     _require(cos.shape[1] == D // 2, "freqs must have D/2 columns")
     L = _lib.lib()
     NB = (S + 63) // 64
     q = torch.empty(B, S, H, D, dtype=torch.bfloat16, device=dev)
-    k = torch.empty_like(q)
-    qsum = torch.empty(B, H, NB, D, dtype=torch.float32, device=dev)
-    ksum = torch.empty_like(qsum)
+    k = torch.empty_like(q) if yk is not None else None
+    qsum = torch.empty(B, H, NB, D, dtype=torch.float32, device=dev) if want_sums else None
+    ksum = torch.empty_like(qsum) if (want_sums and yk is not None) else None
     gate = None
     a_args = [None, _lib.F32, 0, 0]
     if alpha_logit is not None:
@@ -133,7 +141,7 @@ def wan_qk_prologue(yq: torch.Tensor, yk: torch.Tensor, norm_q_weight: torch.Ten
 def wan_self_attention_core(yq, yk, yv, alpha_logit, norm_q_weight, norm_k_weight, grid_sizes,
                             source_video_grid_sizes, TAG, freqs, num_heads, eps=1e-6,
                             SPARSITY_RATIO=0.0625, srr=0.125, flat_ratio=0.5,
-                            out_dtype=torch.float32, stage_events=None):
+                            out_dtype=torch.float32, stage_events=None, keep_workspace=False):
     """model.py:156-175 between the projections and ``self.o``: returns x [B, S, H, D].
 
     yq, yk, yv: the q / k / v projections [B, S, dim]; alpha_logit: ``self.alpha_1(x)``
@@ -149,10 +157,50 @@ def wan_self_attention_core(yq, yk, yv, alpha_logit, norm_q_weight, norm_k_weigh
     t_seq_len = f * h * w
     v = yv.reshape(B, S, H, D)
     alpha_2 = gate.view(B, S, 1, 1) if gate is not None else 0.0
-    x, _ = _editing_sparse_attention_hip(q, k, v, t_seq_len, alpha_2, SPARSITY_RATIO, srr,
-                                         flat_ratio, presummed=(qsum, ksum), out_dtype=out_dtype,
-                                         stage_events=stage_events)
-    return x
+    x, views = _editing_sparse_attention_hip(q, k, v, t_seq_len, alpha_2, SPARSITY_RATIO, srr,
+                                             flat_ratio, presummed=(qsum, ksum), out_dtype=out_dtype,
+                                             stage_events=stage_events, keep_workspace=keep_workspace)
+    return (x, views) if keep_workspace else x
+
+
+@torch.no_grad()
+def ln_modulate(x: torch.Tensor, shift=None, scale=None, weight=None, bias=None, eps=1e-6,
+                y=None, gate=None, out=True):
+    """The residual / LayerNorm / adaLN step of WanAttentionBlock.forward (model.py:249-270)
+    in one pass (icsa_wan_ln_modulate): with ``y``, x += y * gate in place (x f32, y bf16
+    [B, S, dim], gate f32 [B, dim] or [B, 1, dim]); then, unless ``out=False``, returns
+    bf16(LN(x) [* weight + bias] [* (1 + scale) + shift])."""
+    _require(x.is_cuda and x.dim() == 3 and x.stride(-1) == 1, "x must be [B, S, dim], rows contiguous")
+    B, S, dim = x.shape
+
+    def vec(t):
+        if t is None:
+            return None
+        t = t.detach().to(device=x.device, dtype=torch.float32).reshape(B, dim) \
+            if t.numel() == B * dim else t.detach().to(device=x.device, dtype=torch.float32).reshape(dim)
+        return t.contiguous()
+
+    shift, scale, gate = vec(shift), vec(scale), vec(gate)
+    if gate is not None and gate.dim() == 1:
+        gate = gate.expand(B, dim)
+    wt = weight.detach().to(device=x.device, dtype=torch.float32).contiguous() if weight is not None else None
+    bs = bias.detach().to(device=x.device, dtype=torch.float32).contiguous() if bias is not None else None
+    if y is not None:
+        _require(x.dtype == torch.float32, "the residual stream updated in place must be float32")
+        _require(y.shape == x.shape and y.dtype == torch.bfloat16, "y must be bf16 like x")
+        y = y if y.stride(-1) == 1 else y.contiguous()
+    o = torch.empty(B, S, dim, dtype=torch.bfloat16, device=x.device) if out else None
+    rc = _lib.lib().icsa_wan_ln_modulate(
+        ptr(x), dtype_code(x), x.stride(0), x.stride(1),
+        ptr(y), y.stride(0) if y is not None else 0, y.stride(1) if y is not None else 0,
+        ptr(gate), gate.stride(0) if gate is not None else 0,
+        ptr(x) if y is not None else None, x.stride(0), x.stride(1),
+        ptr(wt), ptr(bs),
+        ptr(shift), ptr(scale), shift.stride(0) if shift is not None else 0, float(eps),
+        B, S, dim, ptr(o), o.stride(0) if o is not None else 0, o.stride(1) if o is not None else 0,
+        stream_ptr(x.device))
+    _lib.check("icsa_wan_ln_modulate", rc)
+    return o
 
 
 class WanRMSNorm(nn.Module):
@@ -196,14 +244,123 @@ class WanSelfAttention(nn.Module):
         self.norm_q = WanRMSNorm(dim, eps=eps)
         self.norm_k = WanRMSNorm(dim, eps=eps)
 
+    capture = None    # a dict here receives the workspace views (decisions) of the next call
+
     def forward(self, x, seq_lens, grid_sizes, source_video_grid_sizes, TAG, freqs):
         b, s = x.shape[:2]
-        x_att = wan_self_attention_core(
+        res = wan_self_attention_core(
             self.q(x), self.k(x), self.v(x), self.alpha_1(x), self.norm_q.weight,
             self.norm_k.weight, grid_sizes, source_video_grid_sizes, TAG, freqs,
-            self.num_heads, self.eps)
-        return self.o(x_att.flatten(2).to(x.dtype))
+            self.num_heads, self.eps, keep_workspace=self.capture is not None)
+        if self.capture is not None:
+            res, self.capture["views"] = res
+        return self.o(res.flatten(2).to(x.dtype))
+
+
+class WanLayerNorm(nn.LayerNorm):
+    """Parameter holder of the reference's WanLayerNorm (model.py:117-122); applied by
+    ``ln_modulate``."""
+
+    def __init__(self, dim, eps=1e-6, elementwise_affine=False):
+        super().__init__(dim, elementwise_affine=elementwise_affine, eps=eps)
+
+
+class WanT2VCrossAttention(nn.Module):
+    """WanT2VCrossAttention (model.py:180-188): q / k RMSNorm through the producer in its
+    single-tensor, unrotated mode, dense attention over the text tokens through
+    ``icsa_flash_attn``.  Same parameters as the reference class."""
+
+    def __init__(self, dim, num_heads, window_size=(-1, -1), qk_norm=True, eps=1e-6):
+        super().__init__()
+        self.dim = dim
+        self.num_heads = num_heads
+        self.head_dim = dim // num_heads
+        self.eps = eps
+        _require(qk_norm, "the HIP producer applies the q / k RMSNorm (qk_norm=True)")
+        self.q = nn.Linear(dim, dim)
+        self.k = nn.Linear(dim, dim)
+        self.v = nn.Linear(dim, dim)
+        self.o = nn.Linear(dim, dim)
+        self.alpha_1 = nn.Linear(dim, 1, bias=False)       # unused here, as in the reference
+        self.alpha_2 = nn.Linear(dim, 1, bias=False)
+        self.norm_q = WanRMSNorm(dim, eps=eps)
+        self.norm_k = WanRMSNorm(dim, eps=eps)
+
+    def forward(self, x, context, context_lens=None):
+        _require(context_lens is None, "variable text lengths (context_lens) are not supported")
+        b = x.shape[0]
+        none = [(0, 0, 0)] * b
+        no_rope = _identity_freqs(self.head_dim, x.device)
+        q = wan_qk_prologue(self.q(x), None, self.norm_q.weight, None, none, none, 0, no_rope,
+                            self.num_heads, eps=self.eps, want_sums=False)[0]
+        k = wan_qk_prologue(self.k(context), None, self.norm_k.weight, None, none, none, 0,
+                            no_rope, self.num_heads, eps=self.eps, want_sums=False)[0]
+        v = self.v(context).view(b, -1, self.num_heads, self.head_dim).to(torch.bfloat16)
+        from .hip_host import flash_attn_func
+        y = flash_attn_func(q, k, v)
+        return self.o(y.flatten(2).to(x.dtype))
+
+
+_id_freqs: dict = {}
+
+
+def _identity_freqs(head_dim, device):
+    key = (head_dim, str(device))
+    if key not in _id_freqs:
+        _id_freqs[key] = torch.ones(1, head_dim // 2, dtype=torch.complex128)
+    return _id_freqs[key]
+
+
+class WanAttentionBlock(nn.Module):
+    """WanAttentionBlock (model.py:224-270) on the HIP backend: same constructor, parameters
+    and ``forward(x, e, seq_lens, grid_sizes, freqs, context, context_lens,
+    source_video_grid_sizes, TAG)``.  The residual stream is float32 as in the reference;
+    every residual update + LayerNorm + adaLN modulation is one ``ln_modulate`` pass, the
+    projections and the FFN are library GEMMs, the attentions run in libicsa.so.
+    Only the t2v cross attention is part of this build."""
+
+    def __init__(self, cross_attn_type, dim, ffn_dim, num_heads, window_size=(-1, -1),
+                 qk_norm=True, cross_attn_norm=False, eps=1e-6, backend=Backend.HIP):
+        super().__init__()
+        _require(cross_attn_type == 't2v_cross_attn', "only t2v_cross_attn is supported")
+        self.dim = dim
+        self.ffn_dim = ffn_dim
+        self.num_heads = num_heads
+        self.window_size = window_size
+        self.qk_norm = qk_norm
+        self.cross_attn_norm = cross_attn_norm
+        self.eps = eps
+        self.norm1 = WanLayerNorm(dim, eps)
+        self.self_attn = WanSelfAttention(dim, num_heads, window_size, qk_norm, eps, backend=backend)
+        self.norm3 = WanLayerNorm(dim, eps, elementwise_affine=True) if cross_attn_norm else nn.Identity()
+        self.cross_attn = WanT2VCrossAttention(dim, num_heads, (-1, -1), qk_norm, eps)
+        self.norm2 = WanLayerNorm(dim, eps)
+        self.ffn = nn.Sequential(nn.Linear(dim, ffn_dim), nn.GELU(approximate='tanh'),
+                                 nn.Linear(ffn_dim, dim))
+        self.modulation = nn.Parameter(torch.randn(1, 6, dim) / dim ** 0.5)
+
+    def forward(self, x, e, seq_lens, grid_sizes, freqs, context, context_lens,
+                source_video_grid_sizes, TAG):
+        _require(e.dtype == torch.float32, "e must be float32 (model.py:250)")
+        em = (self.modulation.float() + e).chunk(6, dim=1)           # 6 x [B, 1, dim]
+        x = x.float().contiguous()                                   # residual stream (a copy)
+        h = ln_modulate(x, shift=em[0], scale=em[1], eps=self.eps)   # norm1, modulate
+        y = self.self_attn(h, seq_lens, grid_sizes, source_video_grid_sizes, TAG, freqs)
+        if isinstance(self.norm3, nn.Identity):
+            ln_modulate(x, y=y, gate=em[2], out=False)
+            h = x.to(torch.bfloat16)
+        else:                                                        # x += y e2, norm3
+            h = ln_modulate(x, y=y, gate=em[2], weight=self.norm3.weight, bias=self.norm3.bias,
+                            eps=self.eps)
+        y = self.cross_attn(h, context.to(h.dtype), context_lens)
+        ones = torch.ones(x.shape[0], self.dim, device=x.device)
+        h = ln_modulate(x, y=y.to(torch.bfloat16), gate=ones, shift=em[3], scale=em[4],
+                        eps=self.eps)                                # x += cross, norm2, modulate
+        y = self.ffn(h)
+        ln_modulate(x, y=y.to(torch.bfloat16), gate=em[5], out=False)   # x += ffn e5
+        return x
 
 
 __all__ = ["rope_params", "wan_freqs", "rope_tables", "wan_qk_prologue", "wan_self_attention_core",
-           "WanSelfAttention", "WanRMSNorm"]
+           "ln_modulate", "WanSelfAttention", "WanT2VCrossAttention", "WanAttentionBlock",
+           "WanRMSNorm", "WanLayerNorm"]

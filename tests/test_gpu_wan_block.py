@@ -1,0 +1,82 @@
+"""GPU parity of the Wan DiT block on the HIP backend (in_context_sparse_attention.wan).
+
+* ``ln_modulate`` (icsa_wan_ln_modulate) against float64 LayerNorm / adaLN / residual.
+* ``WanAttentionBlock`` end to end against oracle.wan_block on the GPU's own self-attention
+  decisions.  Bar: the block output is the float32 residual stream of O(1) values after five
+  bf16 GEMM stages; the oracle rounds at the same points but accumulates in float64, so a
+  bf16 rounding flip in a GEMM output may propagate.  Tolerance: max-abs 3e-2 and mean-abs
+  3e-3 (about 4 and 0.4 bf16 ulps of the typical |x| ~ 1).
+"""
+import math
+
+import pytest
+import torch
+
+from oracle import wan_block as WB
+from oracle import wan_glue as W
+from in_context_sparse_attention import wan
+from parity import gpu_decisions
+from test_wan_block_oracle import _params
+
+pytestmark = pytest.mark.gpu
+
+
+def test_ln_modulate_matches_float64(gpu):
+    torch.manual_seed(0)
+    B, S, dim = 2, 37, 5120
+    x = torch.randn(B, S, dim, device=gpu) * 2 + 0.5
+    y = torch.randn(B, S, dim, device=gpu).to(torch.bfloat16)
+    gate = torch.randn(B, 1, dim, device=gpu) * 0.3
+    shift = torch.randn(B, 1, dim, device=gpu) * 0.2
+    scale = torch.randn(B, 1, dim, device=gpu) * 0.2
+    w = torch.rand(dim, device=gpu) + 0.5
+    bb = torch.randn(dim, device=gpu) * 0.1
+    x64 = x.double().cpu()
+    xu = x64 + y.double().cpu() * gate.double().cpu()
+    out = wan.ln_modulate(x, shift=shift, scale=scale, weight=w, bias=bb, y=y, gate=gate)
+    torch.cuda.synchronize()
+    assert torch.allclose(x.double().cpu(), xu, rtol=1e-6, atol=1e-6), "residual update"
+    mean = xu.mean(-1, keepdim=True)
+    ln = (xu - mean) / torch.sqrt((xu - mean).pow(2).mean(-1, keepdim=True) + 1e-6)
+    ref = (ln * w.double().cpu() + bb.double().cpu()) * (1 + scale.double().cpu()) + shift.double().cpu()
+    d = (out.double().cpu() - ref).abs()
+    assert (d <= ref.abs() * 2.0 ** -8 + 1e-6).all(), d.max().item()
+    # update only, and a plain LayerNorm + modulation of a bf16 x (rounded after the norm)
+    xb = torch.randn(B, S, dim, device=gpu).to(torch.bfloat16)
+    o2 = wan.ln_modulate(xb, shift=shift, scale=scale)
+    xb64 = xb.double().cpu()
+    m = xb64.mean(-1, keepdim=True)
+    n = ((xb64 - m) / torch.sqrt((xb64 - m).pow(2).mean(-1, keepdim=True) + 1e-6))
+    ref2 = n.to(torch.bfloat16).double() * (1 + scale.double().cpu()) + shift.double().cpu()
+    d2 = (o2.double().cpu() - ref2).abs()
+    # two roundings: a flip of bf16(n) moves the result by one ulp of n times (1 + scale)
+    bound = (n.abs() * (1 + scale.double().cpu()).abs() + ref2.abs()) * 2.0 ** -7 + 1e-6
+    assert (d2 <= bound).all(), d2.max().item()
+
+
+def test_block_matches_oracle(gpu):
+    dim, ffn, H = 256, 512, 2
+    grid = (2, 16, 16)
+    S = 2 * math.prod(grid)
+    print(f"[block] dim={dim} ffn={ffn} H={H} S={S}", flush=True)
+    P = _params(dim, ffn, 3)
+    blk = wan.WanAttentionBlock("t2v_cross_attn", dim, ffn, H, cross_attn_norm=True)
+    blk.load_state_dict({k: v.float() for k, v in P.items()}, strict=True)
+    blk = blk.to(gpu).to(torch.bfloat16)
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(1, S, dim, generator=g)
+    e = torch.randn(1, 6, dim, generator=g) * 0.1
+    ctx = torch.randn(1, 24, dim, generator=g).to(torch.bfloat16)
+    freqs = W.wan_freqs(128)
+    blk.self_attn.capture = {}
+    out = blk(x.to(gpu), e.to(gpu), torch.tensor([S]), [grid], freqs, ctx.to(gpu), None, [grid], 1)
+    torch.cuda.synchronize()
+    dec = gpu_decisions(blk.self_attn.capture["views"])
+    blk.self_attn.capture = None
+    Pb = {k: v.detach().cpu() for k, v in blk.state_dict().items()}    # the bf16 values used
+    ref, _ = WB.wan_block_forward(Pb, x, e, ctx, grid, grid, 1, freqs, H, decisions=dec)
+    d = (out.double().cpu() - ref).abs()
+    mx, mn = d.max().item(), d.mean().item()
+    print(f"[block] max_abs={mx:.3e} mean_abs={mn:.3e} |x|max={ref.abs().max().item():.2f}", flush=True)
+    assert torch.isfinite(out).all()
+    assert mx <= 3e-2 and mn <= 3e-3, (mx, mn)
