@@ -318,6 +318,58 @@ def block_bench(steps, warmup, log_fn):
     return res
 
 
+def dit_step_bench(steps, log_fn):
+    """Configuration 5: one denoising step of the full Wan 2.2 14B DiT (40 blocks, dim 5120,
+    FFN 13,824, 40 heads; bf16 weights with the reference's init_weights) at 720p: 21 x 90 x
+    160 latents (16 channels) give 21 x 45 x 80 = 75,600 tokens per video, 151,200 target +
+    source tokens; classifier-free guidance as one batch of 2 (conditional and unconditional
+    prompt, 512 text tokens of dim 4096 each); the guidance combination is included, the
+    scheduler update (an elementwise step on the latent) is not."""
+    import torch
+    from in_context_sparse_attention import wan
+    dev = torch.device("cuda:0")
+    torch.manual_seed(0)
+    prev = torch.get_default_dtype()
+    torch.set_default_dtype(torch.bfloat16)
+    try:
+        with torch.device(dev):
+            m = wan.WanModel()                     # the 14B configuration (model.py:299-333 defaults)
+            m.init_weights()
+    finally:
+        torch.set_default_dtype(prev)
+    m.eval()
+    n_params = sum(p_.numel() for p_ in m.parameters())
+    lat = torch.randn(16, 21, 90, 160, device=dev)
+    src = torch.randn(16, 21, 90, 160, device=dev).to(torch.bfloat16)
+    ctx = [torch.randn(512, 4096, device=dev).to(torch.bfloat16) for _ in range(2)]
+    seq_len = 2 * 21 * 45 * 80
+    guide = 5.0
+
+    def step(t):
+        with torch.no_grad():
+            out = m([lat.to(torch.bfloat16)] * 2, t, ctx, seq_len, [src] * 2)
+            return guide * (out[1] - out[0]) + out[0]
+
+    ts = torch.rand(steps + 1, device=dev) * 1000
+    step(ts[:1])                                   # warmup
+    torch.cuda.synchronize()
+    times = []
+    for i in range(steps):
+        t0 = time.perf_counter()
+        step(ts[i + 1:i + 2])
+        torch.cuda.synchronize()
+        times.append(time.perf_counter() - t0)
+    ms = statistics.mean(times) * 1e3
+    res = {"step_ms": ms, "steps_timed": steps, "params": n_params,
+           "workload": ("configuration 5: one CFG denoising step (batch of 2) of the 40-block "
+                        "Wan 2.2 14B DiT, 720p 81-frame latents, 151,200 target + source tokens, "
+                        "512 text tokens, bf16 random-init weights")}
+    log_fn(f"[bench] DiT step (cfg 5): {ms:.0f} ms per step ({n_params / 1e9:.2f} B parameters)")
+    del m
+    torch.cuda.empty_cache()
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -340,6 +392,9 @@ def main():
                     help="skip the configuration-4 DiT block leg")
     ap.add_argument("--block-only", action="store_true",
                     help="run only the configuration-4 DiT block leg (for profiling)")
+    ap.add_argument("--dit-step", action="store_true",
+                    help="run only configuration 5: one CFG denoising step of the 40-block DiT "
+                         "(several seconds per step; --steps timed steps after one warmup)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
                     help="after the timed steps, run 3 elementwise copies (torch.neg) of BYTES "
                          "bytes: the reference kernel of known traffic that scales the HBM "
@@ -361,6 +416,9 @@ def main():
     _lib.lib()
     if args.wan_only:
         print(json.dumps({"wan_attention": wan_attention_bench(args.steps, args.warmup, log)}), flush=True)
+        return
+    if args.dit_step:
+        print(json.dumps({"dit_step": dit_step_bench(max(1, args.steps), log)}), flush=True)
         return
     if args.block_only:
         print(json.dumps({"dit_block": block_bench(args.steps, args.warmup, log)}), flush=True)

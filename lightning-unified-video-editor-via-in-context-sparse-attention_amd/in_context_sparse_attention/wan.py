@@ -174,15 +174,16 @@ def ln_modulate(x: torch.Tensor, shift=None, scale=None, weight=None, bias=None,
     B, S, dim = x.shape
 
     def vec(t):
+        """[B, dim] f32 view; one [dim] row broadcast over the batch has batch stride 0."""
         if t is None:
             return None
-        t = t.detach().to(device=x.device, dtype=torch.float32).reshape(B, dim) \
-            if t.numel() == B * dim else t.detach().to(device=x.device, dtype=torch.float32).reshape(dim)
-        return t.contiguous()
+        t = t.detach().to(device=x.device, dtype=torch.float32)
+        if t.numel() == B * dim:
+            return t.reshape(B, dim).contiguous()
+        _require(t.numel() == dim, "modulation / gate vectors must be [B, dim] or [dim]")
+        return t.reshape(1, dim).contiguous().expand(B, dim)
 
     shift, scale, gate = vec(shift), vec(scale), vec(gate)
-    if gate is not None and gate.dim() == 1:
-        gate = gate.expand(B, dim)
     wt = weight.detach().to(device=x.device, dtype=torch.float32).contiguous() if weight is not None else None
     bs = bias.detach().to(device=x.device, dtype=torch.float32).contiguous() if bias is not None else None
     if y is not None:
@@ -343,8 +344,10 @@ class WanAttentionBlock(nn.Module):
                 source_video_grid_sizes, TAG):
         _require(e.dtype == torch.float32, "e must be float32 (model.py:250)")
         em = (self.modulation.float() + e).chunk(6, dim=1)           # 6 x [B, 1, dim]
-        x = x.float().contiguous()                                   # residual stream (a copy)
-        h = ln_modulate(x, shift=em[0], scale=em[1], eps=self.eps)   # norm1, modulate
+        x = x if x.stride(-1) == 1 else x.contiguous()
+        # norm1, modulate; a bf16 x (the first block) rounds the LayerNorm to bf16 (.type_as)
+        h = ln_modulate(x, shift=em[0], scale=em[1], eps=self.eps)
+        x = x.to(torch.float32, copy=True)                           # residual stream (a copy)
         y = self.self_attn(h, seq_lens, grid_sizes, source_video_grid_sizes, TAG, freqs)
         if isinstance(self.norm3, nn.Identity):
             ln_modulate(x, y=y, gate=em[2], out=False)
@@ -361,6 +364,150 @@ class WanAttentionBlock(nn.Module):
         return x
 
 
+def sinusoidal_embedding_1d(dim, position):
+    """model.py:26-31: [len(position), dim] float64 cos / sin embedding."""
+    assert dim % 2 == 0
+    half = dim // 2
+    position = position.type(torch.float64)
+    sinusoid = torch.outer(position, torch.pow(10000, -torch.arange(half).to(position).div(half)))
+    return torch.cat([torch.cos(sinusoid), torch.sin(sinusoid)], dim=1)
+
+
+class Head(nn.Module):
+    """Head (model.py:274-288): LayerNorm, modulation and the output Linear, in fp32 as the
+    reference's autocast(float32) region."""
+
+    def __init__(self, dim, out_dim, patch_size, eps=1e-6):
+        super().__init__()
+        self.dim = dim
+        self.out_dim = out_dim
+        self.patch_size = patch_size
+        self.eps = eps
+        out_dim = math.prod(patch_size) * out_dim
+        self.norm = WanLayerNorm(dim, eps)
+        self.head = nn.Linear(dim, out_dim)
+        self.modulation = nn.Parameter(torch.randn(1, 2, dim) / dim ** 0.5)
+
+    def forward(self, x, e):
+        e = (self.modulation.float() + e.float().unsqueeze(1)).chunk(2, dim=1)
+        n = nn.functional.layer_norm(x.float(), (self.dim,), eps=self.eps)
+        return nn.functional.linear(n * (1 + e[1]) + e[0], self.head.weight.float(),
+                                    self.head.bias.float())
+
+
+class WanModel(nn.Module):
+    """WanModel (model.py:299-466), t2v, on the HIP backend: same constructor arguments,
+    parameter names and ``forward(x, t, context, seq_len, source_video_latent)``.
+
+    The blocks are ``WanAttentionBlock`` above.  The (1, 2, 2) patch embeddings run as a
+    reshape and a library GEMM (kernel = stride), the text / time embeddings and the head
+    as in the reference.  Several inputs in the lists (e.g. the conditional and the
+    unconditional pass of classifier-free guidance) run as one batch."""
+
+    def __init__(self, model_type='t2v', patch_size=(1, 2, 2), text_len=512, in_dim=16, dim=5120,
+                 ffn_dim=13824, freq_dim=256, text_dim=4096, out_dim=16, num_heads=40,
+                 num_layers=40, window_size=(-1, -1), qk_norm=True, cross_attn_norm=True,
+                 eps=1e-6, use_siglip=False, use_riflex=False, backend=Backend.HIP):
+        super().__init__()
+        _require(model_type == 't2v', "only the t2v model is part of this build")
+        self.model_type = model_type
+        self.backend = backend
+        self.patch_size = patch_size
+        self.source_video_patch_size = patch_size
+        self.text_len = text_len
+        self.in_dim = in_dim
+        self.dim = dim
+        self.ffn_dim = ffn_dim
+        self.freq_dim = freq_dim
+        self.text_dim = text_dim
+        self.out_dim = out_dim
+        self.num_heads = num_heads
+        self.num_layers = num_layers
+        self.window_size = window_size
+        self.qk_norm = qk_norm
+        self.cross_attn_norm = cross_attn_norm
+        self.eps = eps
+        self.patch_embedding = nn.Conv3d(in_dim, dim, kernel_size=patch_size, stride=patch_size)
+        self.source_video_embedding_more_memory = nn.Conv3d(
+            in_dim, dim, kernel_size=patch_size, stride=patch_size)
+        self.text_embedding = nn.Sequential(
+            nn.Linear(text_dim, dim), nn.GELU(approximate='tanh'), nn.Linear(dim, dim))
+        self.time_embedding = nn.Sequential(nn.Linear(freq_dim, dim), nn.SiLU(), nn.Linear(dim, dim))
+        self.time_projection = nn.Sequential(nn.SiLU(), nn.Linear(dim, dim * 6))
+        self.blocks = nn.ModuleList([
+            WanAttentionBlock('t2v_cross_attn', dim, ffn_dim, num_heads, window_size, qk_norm,
+                              cross_attn_norm, eps, backend=backend)
+            for _ in range(num_layers)])
+        self.head = Head(dim, out_dim, patch_size, eps)
+        d = dim // num_heads
+        assert (dim % num_heads) == 0 and d % 2 == 0
+        self.freqs = wan_freqs(d)
+
+    def init_weights(self):
+        """model.py:387-397."""
+        for m in self.modules():
+            if isinstance(m, nn.Linear):
+                nn.init.xavier_uniform_(m.weight)
+                if m.bias is not None:
+                    nn.init.zeros_(m.bias)
+        nn.init.xavier_uniform_(self.patch_embedding.weight.flatten(1))
+        for m in self.text_embedding.modules():
+            if isinstance(m, nn.Linear):
+                nn.init.normal_(m.weight, std=0.02)
+        for m in self.time_embedding.modules():
+            if isinstance(m, nn.Linear):
+                nn.init.normal_(m.weight, std=0.02)
+        nn.init.zeros_(self.head.head.weight)
+
+    def _patchify(self, conv, u):
+        """Conv3d with kernel = stride as a GEMM: [C, F, H, W] -> [F*(H/ph)*(W/pw), dim]."""
+        pf, ph, pw = self.patch_size
+        C, F_, H_, W_ = u.shape
+        g = (F_ // pf, H_ // ph, W_ // pw)
+        p = u.reshape(C, g[0], pf, g[1], ph, g[2], pw).permute(1, 3, 5, 0, 2, 4, 6)
+        p = p.reshape(g[0] * g[1] * g[2], C * pf * ph * pw)
+        w = conv.weight.reshape(self.dim, -1)
+        return nn.functional.linear(p.to(w.dtype), w, conv.bias), g
+
+    def forward(self, x, t, context, seq_len, source_video_latent):
+        dev = self.patch_embedding.weight.device
+        xs, grids = zip(*[self._patchify(self.patch_embedding, u) for u in x])
+        ss, sgrids = zip(*[self._patchify(self.source_video_embedding_more_memory, u)
+                           for u in source_video_latent])
+        s_lens = [u.shape[0] for u in ss]
+        rows = [torch.cat([u, v], dim=0) for u, v in zip(xs, ss)]
+        _require(max(r.shape[0] for r in rows) <= seq_len, "seq_len smaller than the token count")
+        xb = torch.stack([torch.cat([r, r.new_zeros(seq_len - r.shape[0], self.dim)]) for r in rows])
+        def f32_linear(lin, z):                  # the reference's autocast(float32) region
+            return nn.functional.linear(z, lin.weight.float(), lin.bias.float())
+
+        temb = sinusoidal_embedding_1d(self.freq_dim, t).float().to(dev)
+        e = f32_linear(self.time_embedding[2],
+                       nn.functional.silu(f32_linear(self.time_embedding[0], temb)))
+        e0 = f32_linear(self.time_projection[1], nn.functional.silu(e)).unflatten(1, (6, self.dim))
+        ctx = self.text_embedding(torch.stack([
+            torch.cat([u, u.new_zeros(self.text_len - u.size(0), u.size(1))]) for u in context]).to(
+                self.text_embedding[0].weight.dtype))
+        seq_lens = torch.tensor([r.shape[0] for r in rows], dtype=torch.long)
+        h = xb
+        for block in self.blocks:
+            h = block(h, e0, seq_lens, list(grids), self.freqs, ctx, None, list(sgrids), 1)
+        h = torch.stack([u[:u.shape[0] - s_lens[i]] for i, u in enumerate(h)], 0)
+        out = self.head(h, e)
+        return self.unpatchify(out, grids)
+
+    def unpatchify(self, x, grid_sizes):
+        """model.py:455-466."""
+        c = self.out_dim
+        out = []
+        for u, v in zip(x, grid_sizes):
+            u = u[:math.prod(v)].view(*v, *self.patch_size, c)
+            u = torch.einsum('fhwpqrc->cfphqwr', u)
+            u = u.reshape(c, *[i * j for i, j in zip(v, self.patch_size)])
+            out.append(u)
+        return out
+
+
 __all__ = ["rope_params", "wan_freqs", "rope_tables", "wan_qk_prologue", "wan_self_attention_core",
            "ln_modulate", "WanSelfAttention", "WanT2VCrossAttention", "WanAttentionBlock",
-           "WanRMSNorm", "WanLayerNorm"]
+           "WanRMSNorm", "WanLayerNorm", "Head", "WanModel", "sinusoidal_embedding_1d"]

@@ -58,9 +58,11 @@ def layer_norm(x, eps, w=None, b=None):
 
 
 def wan_block_forward(P: dict, x, e, context, grid, src_grid, tag, freqs, num_heads, eps=1e-6,
-                      decisions=None, sparsity=0.0625):
+                      decisions=None, sparsity=0.0625, x_is_bf16=False):
     """One block on float64 tensors.  P: the block's state dict (reference parameter names).
-    x [B, S, dim], e [B, 6, dim], context [B, L, dim].  Returns (x, path-oracle info)."""
+    x [B, S, dim], e [B, 6, dim], context [B, L, dim].  ``x_is_bf16``: the block input is the
+    bf16 patch embedding (the model's first block), so norm1's ``.type_as(x)`` rounds the
+    LayerNorm to bf16.  Returns (x, path-oracle info)."""
     B, S, dim = x.shape
     H = num_heads
     D = dim // H
@@ -70,7 +72,8 @@ def wan_block_forward(P: dict, x, e, context, grid, src_grid, tag, freqs, num_he
     em = (p["modulation"] + e.detach().cpu().double()).chunk(6, dim=1)
 
     # self attention on norm1(x) * (1 + e1) + e0 (model.py:255-257)
-    h = layer_norm(x, eps) * (1 + em[1]) + em[0]
+    n1 = layer_norm(x, eps)
+    h = (bf(n1) if x_is_bf16 else n1) * (1 + em[1]) + em[0]
     yq = linear(h, p["self_attn.q.weight"], p["self_attn.q.bias"])
     yk = linear(h, p["self_attn.k.weight"], p["self_attn.k.bias"])
     yv = linear(h, p["self_attn.v.weight"], p["self_attn.v.bias"])
