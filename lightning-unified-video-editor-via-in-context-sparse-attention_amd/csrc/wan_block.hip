@@ -90,9 +90,11 @@ __global__ void __launch_bounds__(LNM_THREADS) icsa_wan_ln_mod_kernel(LnModParam
 #pragma unroll
       for (int e = 0; e < 4; ++e) o[e] = fmaf(o[e], w[e], bb[e]);
     }
-    if constexpr (sizeof(TX) == 2) {                    // .type_as(x) of a bf16 x
+    if constexpr (sizeof(TX) == 2) {                    // .type_as(x) of a bf16 x; after an
+      if (p.y == nullptr) {                             // update x + y * gate is f32 (promotion)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) o[e] = (float)(bf16)o[e];
+        for (int e = 0; e < 4; ++e) o[e] = (float)(bf16)o[e];
+      }
     }
     if (p.scale != nullptr) {                           // * (1 + scale) + shift
       const floatx4 sc = *reinterpret_cast<const floatx4*>(p.scale + (int64_t)b * p.mod_sb + 4 * c);

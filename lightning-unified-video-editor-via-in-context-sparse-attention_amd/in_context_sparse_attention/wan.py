@@ -165,11 +165,13 @@ def wan_self_attention_core(yq, yk, yv, alpha_logit, norm_q_weight, norm_k_weigh
 
 @torch.no_grad()
 def ln_modulate(x: torch.Tensor, shift=None, scale=None, weight=None, bias=None, eps=1e-6,
-                y=None, gate=None, out=True):
+                y=None, gate=None, out=True, x_out=None):
     """The residual / LayerNorm / adaLN step of WanAttentionBlock.forward (model.py:249-270)
-    in one pass (icsa_wan_ln_modulate): with ``y``, x += y * gate in place (x f32, y bf16
-    [B, S, dim], gate f32 [B, dim] or [B, 1, dim]); then, unless ``out=False``, returns
-    bf16(LN(x) [* weight + bias] [* (1 + scale) + shift])."""
+    in one pass (icsa_wan_ln_modulate): with ``y``, x += y * gate (y bf16 [B, S, dim], gate
+    f32 [B, dim] or [B, 1, dim]), in place for an f32 x, or into the f32 ``x_out`` (then x
+    may be bf16 and is left unchanged); then, unless ``out=False``, returns
+    bf16(LN(x) [* weight + bias] [* (1 + scale) + shift]).  A bf16 x without ``y`` rounds
+    the LayerNorm to bf16 (WanLayerNorm's ``.type_as(x)``); an updated x is f32 and does not."""
     _require(x.is_cuda and x.dim() == 3 and x.stride(-1) == 1, "x must be [B, S, dim], rows contiguous")
     B, S, dim = x.shape
 
@@ -187,15 +189,22 @@ def ln_modulate(x: torch.Tensor, shift=None, scale=None, weight=None, bias=None,
     wt = weight.detach().to(device=x.device, dtype=torch.float32).contiguous() if weight is not None else None
     bs = bias.detach().to(device=x.device, dtype=torch.float32).contiguous() if bias is not None else None
     if y is not None:
-        _require(x.dtype == torch.float32, "the residual stream updated in place must be float32")
+        if x_out is None:
+            _require(x.dtype == torch.float32, "the residual stream updated in place must be float32")
+            x_out = x
+        _require(x_out.dtype == torch.float32 and x_out.shape == x.shape and x_out.stride(-1) == 1,
+                 "x_out must be float32 like x, rows contiguous")
         _require(y.shape == x.shape and y.dtype == torch.bfloat16, "y must be bf16 like x")
         y = y if y.stride(-1) == 1 else y.contiguous()
+    else:
+        _require(x_out is None, "x_out needs y")
     o = torch.empty(B, S, dim, dtype=torch.bfloat16, device=x.device) if out else None
     rc = _lib.lib().icsa_wan_ln_modulate(
         ptr(x), dtype_code(x), x.stride(0), x.stride(1),
         ptr(y), y.stride(0) if y is not None else 0, y.stride(1) if y is not None else 0,
         ptr(gate), gate.stride(0) if gate is not None else 0,
-        ptr(x) if y is not None else None, x.stride(0), x.stride(1),
+        ptr(x_out), x_out.stride(0) if x_out is not None else 0,
+        x_out.stride(1) if x_out is not None else 0,
         ptr(wt), ptr(bs),
         ptr(shift), ptr(scale), shift.stride(0) if shift is not None else 0, float(eps),
         B, S, dim, ptr(o), o.stride(0) if o is not None else 0, o.stride(1) if o is not None else 0,
@@ -252,10 +261,12 @@ class WanSelfAttention(nn.Module):
         res = wan_self_attention_core(
             self.q(x), self.k(x), self.v(x), self.alpha_1(x), self.norm_q.weight,
             self.norm_k.weight, grid_sizes, source_video_grid_sizes, TAG, freqs,
-            self.num_heads, self.eps, keep_workspace=self.capture is not None)
+            self.num_heads, self.eps, out_dtype=x.dtype, keep_workspace=self.capture is not None)
         if self.capture is not None:
             res, self.capture["views"] = res
-        return self.o(res.flatten(2).to(x.dtype))
+        # the kernels add the residual in f32 and round once at the store, which equals the
+        # reference's f32 result cast to the projection's dtype
+        return self.o(res.flatten(2))
 
 
 class WanLayerNorm(nn.LayerNorm):
@@ -347,14 +358,15 @@ class WanAttentionBlock(nn.Module):
         x = x if x.stride(-1) == 1 else x.contiguous()
         # norm1, modulate; a bf16 x (the first block) rounds the LayerNorm to bf16 (.type_as)
         h = ln_modulate(x, shift=em[0], scale=em[1], eps=self.eps)
-        x = x.to(torch.float32, copy=True)                           # residual stream (a copy)
         y = self.self_attn(h, seq_lens, grid_sizes, source_video_grid_sizes, TAG, freqs)
-        if isinstance(self.norm3, nn.Identity):
-            ln_modulate(x, y=y, gate=em[2], out=False)
-            h = x.to(torch.bfloat16)
-        else:                                                        # x += y e2, norm3
+        xs = torch.empty(x.shape, dtype=torch.float32, device=x.device)  # the f32 residual stream
+        if isinstance(self.norm3, nn.Identity):                      # x + y e2 (the input is kept)
+            ln_modulate(x, y=y, gate=em[2], out=False, x_out=xs)
+            h = xs.to(torch.bfloat16)
+        else:                                                        # ... then norm3
             h = ln_modulate(x, y=y, gate=em[2], weight=self.norm3.weight, bias=self.norm3.bias,
-                            eps=self.eps)
+                            eps=self.eps, x_out=xs)
+        x = xs
         y = self.cross_attn(h, context.to(h.dtype), context_lens)
         ones = torch.ones(x.shape[0], self.dim, device=x.device)
         h = ln_modulate(x, y=y.to(torch.bfloat16), gate=ones, shift=em[3], scale=em[4],
@@ -365,7 +377,7 @@ class WanAttentionBlock(nn.Module):
 
 
 def sinusoidal_embedding_1d(dim, position):
-    """model.py:26-31: [len(position), dim] float64 cos / sin embedding."""
+    """model.py:25-31: [len(position), dim] float64 cos / sin embedding."""
     assert dim % 2 == 0
     half = dim // 2
     position = position.type(torch.float64)
@@ -374,7 +386,7 @@ def sinusoidal_embedding_1d(dim, position):
 
 
 class Head(nn.Module):
-    """Head (model.py:274-288): LayerNorm, modulation and the output Linear, in fp32 as the
+    """Head (model.py:272-290): LayerNorm, modulation and the output Linear, in fp32 as the
     reference's autocast(float32) region."""
 
     def __init__(self, dim, out_dim, patch_size, eps=1e-6):
@@ -396,7 +408,7 @@ class Head(nn.Module):
 
 
 class WanModel(nn.Module):
-    """WanModel (model.py:299-466), t2v, on the HIP backend: same constructor arguments,
+    """WanModel (model.py:308-466), t2v, on the HIP backend: same constructor arguments,
     parameter names and ``forward(x, t, context, seq_len, source_video_latent)``.
 
     The blocks are ``WanAttentionBlock`` above.  The (1, 2, 2) patch embeddings run as a
@@ -444,7 +456,7 @@ class WanModel(nn.Module):
         self.freqs = wan_freqs(d)
 
     def init_weights(self):
-        """model.py:387-397."""
+        """model.py:395-408."""
         for m in self.modules():
             if isinstance(m, nn.Linear):
                 nn.init.xavier_uniform_(m.weight)
@@ -497,7 +509,7 @@ class WanModel(nn.Module):
         return self.unpatchify(out, grids)
 
     def unpatchify(self, x, grid_sizes):
-        """model.py:455-466."""
+        """model.py:456-466."""
         c = self.out_dim
         out = []
         for u, v in zip(x, grid_sizes):

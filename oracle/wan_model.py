@@ -4,15 +4,15 @@ TEST INFRASTRUCTURE ONLY -- imported by tests/, never by the HIP product path.
 
 Restated from the reference (paths relative to the reference repository root):
 
-* ``model.py:399-452``  ``WanModel._forward``: patch embeddings of the target and source
+* ``model.py:410-451``  ``WanModel._forward``: patch embeddings of the target and source
                         latents (Conv3d, kernel = stride = patch size), [target | source]
                         concatenation, zero padding to seq_len, sinusoidal time embedding
                         -> time_embedding -> time_projection (float32 region), text
                         embedding of the zero-padded prompts, the blocks, removal of the
                         source tokens, the head and ``unpatchify``.
-* ``model.py:26-31``    ``sinusoidal_embedding_1d``.
-* ``model.py:274-288``  ``Head`` (float32 region).
-* ``model.py:455-466``  ``unpatchify``.
+* ``model.py:25-31``    ``sinusoidal_embedding_1d``.
+* ``model.py:272-290``  ``Head`` (float32 region).
+* ``model.py:456-466``  ``unpatchify``.
 
 Precision: float64 between the rounding points of the model under bf16 autocast (see
 oracle.wan_block); the float32 autocast regions (time embedding, head) are float64 here.

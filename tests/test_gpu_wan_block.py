@@ -52,6 +52,20 @@ def test_ln_modulate_matches_float64(gpu):
     # two roundings: a flip of bf16(n) moves the result by one ulp of n times (1 + scale)
     bound = (n.abs() * (1 + scale.double().cpu()).abs() + ref2.abs()) * 2.0 ** -7 + 1e-6
     assert (d2 <= bound).all(), d2.max().item()
+    # a bf16 x updated into a separate f32 stream: x is kept, x + y * gate is f32, and the
+    # LayerNorm of the updated row is not rounded to bf16 (type promotion in the reference)
+    xb_before = xb.clone()
+    xs = torch.empty(B, S, dim, device=gpu)
+    o3 = wan.ln_modulate(xb, shift=shift, scale=scale, weight=w, bias=bb, y=y, gate=gate, x_out=xs)
+    torch.cuda.synchronize()
+    assert torch.equal(xb, xb_before), "x must be left unchanged when x_out is given"
+    xu3 = xb64 + y.double().cpu() * gate.double().cpu()
+    assert torch.allclose(xs.double().cpu(), xu3, rtol=1e-6, atol=1e-6), "update into x_out"
+    m3 = xu3.mean(-1, keepdim=True)
+    ln3 = (xu3 - m3) / torch.sqrt((xu3 - m3).pow(2).mean(-1, keepdim=True) + 1e-6)
+    ref3 = (ln3 * w.double().cpu() + bb.double().cpu()) * (1 + scale.double().cpu()) + shift.double().cpu()
+    d3 = (o3.double().cpu() - ref3).abs()
+    assert (d3 <= ref3.abs() * 2.0 ** -8 + 1e-6).all(), d3.max().item()
 
 
 def test_block_matches_oracle(gpu):
