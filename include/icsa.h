@@ -40,6 +40,13 @@
  *   icsa_editing_sparse_attention_presummed
  *                                   <- editing_sparse_attention (esa.py:67-232) fed by that
  *                                        producer (q / k block sums already computed)
+ *   icsa_sparse_piecewise_attn_fwd  <- SparsePiecewiseAttn1stIntervalsFunction.forward,
+ *                                        triton_kernels.py:489-539 (output, lse, indices
+ *                                        saved for the backward)
+ *   icsa_sparse_piecewise_attn_bwd  <- SparsePiecewiseAttn1stIntervalsFunction.backward,
+ *                                        triton_kernels.py:541-598, and its kernel
+ *                                        sparse_piecewise_attn_1st_intervals_bwd_kernel
+ *                                        :265-486
  */
 #ifndef ICSA_H_
 #define ICSA_H_
@@ -165,6 +172,40 @@ int icsa_sparse_piecewise_attn(
     int B, int H, int TQ, int TKV, int D, double sparsity,
     const int32_t* inject_idx, int32_t* idx_out,
     void* out, int64_t o_sb, int64_t o_sh, int64_t o_st,
+    void* workspace, int64_t workspace_bytes, void* stream);
+
+/* The same forward (workspace: icsa_sparse_piecewise_workspace_size) with the state its
+ * backward needs: idx_out [B*H, TQ/64, top_k] (required) and lse_out [B*H, TQ] f32
+ * (required), the log-sum-exp in log2 units as the Triton forward stores it: the final
+ * running max of the log2-scaled scores plus log2(l + g_l). */
+int icsa_sparse_piecewise_attn_fwd(
+    const void* q, int64_t q_sb, int64_t q_sh, int64_t q_st,
+    const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st,
+    const void* v, int64_t v_sb, int64_t v_sh, int64_t v_st,
+    int B, int H, int TQ, int TKV, int D, double sparsity,
+    const int32_t* inject_idx, int32_t* idx_out,
+    void* out, int64_t o_sb, int64_t o_sh, int64_t o_st, float* lse_out,
+    void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Workspace bytes of icsa_sparse_piecewise_attn_bwd. */
+int64_t icsa_sparse_piecewise_attn_bwd_workspace_size(int B, int H, int TQ, int TKV, int D);
+
+/* Gradients of icsa_sparse_piecewise_attn_fwd: dout, q, out [B, H, TQ, D] and k, v
+ * [B, H, TKV, D] bf16 (strides sb, sh, st), lse [B*H, TQ] and idx [B*H, TQ/64, top_k]
+ * from the forward (distinct block indices per row; entries outside [0, TKV/64) are
+ * skipped).  dq / dk / dv are written (not accumulated) as bf16 or f32 (dtype codes).
+ * Deterministic: every gradient is a fixed-order sum, no atomics. */
+int icsa_sparse_piecewise_attn_bwd(
+    const void* dout, int64_t do_sb, int64_t do_sh, int64_t do_st,
+    const void* q, int64_t q_sb, int64_t q_sh, int64_t q_st,
+    const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st,
+    const void* v, int64_t v_sb, int64_t v_sh, int64_t v_st,
+    const void* out, int64_t o_sb, int64_t o_sh, int64_t o_st,
+    const float* lse, const int32_t* idx,
+    int B, int H, int TQ, int TKV, int D, int top_k,
+    void* dq, int dq_dtype, int64_t dq_sb, int64_t dq_sh, int64_t dq_st,
+    void* dk, int dk_dtype, int64_t dk_sb, int64_t dk_sh, int64_t dk_st,
+    void* dv, int dv_dtype, int64_t dv_sb, int64_t dv_sh, int64_t dv_st,
     void* workspace, int64_t workspace_bytes, void* stream);
 
 /* Workspace bytes of icsa_flash_attn. */

@@ -380,7 +380,7 @@ int editing_impl(ICSA_EDITING_ARGS, void* const* stage_events, const float* qsum
     s.idx = l3; s.top_k = z.top_k; s.NKV = z.NKV; s.NKVp = z.NKVp;
     s.kc = np.kc; s.vct = np.vct;
     s.out_c = cp.out_c; s.nb_q = z.NB;
-    s.alpha = av; s.out = ov; s.scale_log2 = scale_log2;
+    s.alpha = av; s.out = ov; s.scale_log2 = scale_log2; s.lse = nullptr;
     ICSA_HIP_TRY(launch_sparse(s, stream), "sparse attention");
   }
   ICSA_HIP_TRY(mark(ICSA_STAGE_SPARSE), "event");
@@ -562,13 +562,13 @@ int64_t icsa_sparse_piecewise_workspace_size(int B, int H, int TQ, int TKV, int 
   return sparse_layout(B, H, TQ, TKV, sparsity).total;
 }
 
-int icsa_sparse_piecewise_attn(
+static int sparse_piecewise_impl(
     const void* q, int64_t q_sb, int64_t q_sh, int64_t q_st,
     const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st,
     const void* v, int64_t v_sb, int64_t v_sh, int64_t v_st,
     int B, int H, int TQ, int TKV, int D, double sparsity,
     const int32_t* inject_idx, int32_t* idx_out,
-    void* out, int64_t o_sb, int64_t o_sh, int64_t o_st,
+    void* out, int64_t o_sb, int64_t o_sh, int64_t o_st, float* lse_out,
     void* workspace, int64_t workspace_bytes, void* stream_) {
   int rc = validate_common(B, TQ, H, D);
   if (rc) return rc;
@@ -647,11 +647,175 @@ int icsa_sparse_piecewise_attn(
   s.alpha = make_alpha(nullptr, ICSA_F32, 0, 0, 0, 0, 0.f);
   s.out = OutView{out, o_sb, o_st, o_sh, ICSA_BF16};
   s.scale_log2 = kLog2e / std::sqrt((float)ICSA_D);
+  s.lse = lse_out;
   ICSA_HIP_TRY(launch_sparse(s, stream), "sparse attention");
   return ICSA_OK;
 }
 
+int icsa_sparse_piecewise_attn(
+    const void* q, int64_t q_sb, int64_t q_sh, int64_t q_st,
+    const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st,
+    const void* v, int64_t v_sb, int64_t v_sh, int64_t v_st,
+    int B, int H, int TQ, int TKV, int D, double sparsity,
+    const int32_t* inject_idx, int32_t* idx_out,
+    void* out, int64_t o_sb, int64_t o_sh, int64_t o_st,
+    void* workspace, int64_t workspace_bytes, void* stream) {
+  return sparse_piecewise_impl(q, q_sb, q_sh, q_st, k, k_sb, k_sh, k_st, v, v_sb, v_sh, v_st, B, H,
+                               TQ, TKV, D, sparsity, inject_idx, idx_out, out, o_sb, o_sh, o_st,
+                               nullptr, workspace, workspace_bytes, stream);
+}
+
+int icsa_sparse_piecewise_attn_fwd(
+    const void* q, int64_t q_sb, int64_t q_sh, int64_t q_st,
+    const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st,
+    const void* v, int64_t v_sb, int64_t v_sh, int64_t v_st,
+    int B, int H, int TQ, int TKV, int D, double sparsity,
+    const int32_t* inject_idx, int32_t* idx_out,
+    void* out, int64_t o_sb, int64_t o_sh, int64_t o_st, float* lse_out,
+    void* workspace, int64_t workspace_bytes, void* stream) {
+  if (!idx_out || !lse_out) return fail(ICSA_EINVAL, "idx_out and lse_out are required (saved for the backward)");
+  return sparse_piecewise_impl(q, q_sb, q_sh, q_st, k, k_sb, k_sh, k_st, v, v_sb, v_sh, v_st, B, H,
+                               TQ, TKV, D, sparsity, inject_idx, idx_out, out, o_sb, o_sh, o_st,
+                               lse_out, workspace, workspace_bytes, stream);
+}
+
 // ---------------------------------------------------------------------------------------
+
+}  // extern "C"
+
+namespace {
+struct BwLayout {
+  int64_t ksum, vsum, kt, qt, dot, dvec, selbits, kcb, vcb, kct, dkc, dvc, total;
+  int nsplit, qb_per_split;
+};
+// Interval partials: enough (chunk, query-range) workgroups to fill the GPU, each range at
+// least 8 query blocks long.
+BwLayout bwd_layout(int B, int H, int TQ, int TKV) {
+  const int64_t BH = (int64_t)B * H;
+  const int NQ = TQ / ICSA_BLOCK, NKV = TKV / ICSA_BLOCK;
+  const int nc = ceil_div(NKV, 64), NKVp = nc * 64;
+  BwLayout L;
+  const int want = std::max(1, ceil_div(1024, (int)std::max<int64_t>(1, BH * nc)));
+  int qbps = std::max(8, ceil_div(NQ, want));
+  qbps = std::min(qbps, NQ);
+  L.qb_per_split = qbps;
+  L.nsplit = ceil_div(NQ, qbps);
+  int64_t o = 0;
+  L.ksum = o; o += align256(BH * NKV * ICSA_D * 4);
+  L.vsum = o; o += align256(BH * NKV * ICSA_D * 4);
+  L.kt = o; o += align256(BH * ICSA_D * (int64_t)TKV * 2);
+  L.qt = o; o += align256(BH * ICSA_D * (int64_t)TQ * 2);
+  L.dot = o; o += align256(BH * ICSA_D * (int64_t)TQ * 2);
+  L.dvec = o; o += align256(BH * (int64_t)TQ * 4);
+  L.selbits = o; o += align256(BH * NQ * (int64_t)nc * 8);
+  L.kcb = o; o += align256(BH * NKVp * ICSA_D * 2);
+  L.vcb = o; o += align256(BH * NKVp * ICSA_D * 2);
+  L.kct = o; o += align256(BH * ICSA_D * NKVp * 2);
+  L.dkc = o; o += align256((int64_t)L.nsplit * BH * NKVp * ICSA_D * 4);
+  L.dvc = o; o += align256((int64_t)L.nsplit * BH * NKVp * ICSA_D * 4);
+  L.total = o;
+  return L;
+}
+}  // namespace
+
+extern "C" {
+
+int64_t icsa_sparse_piecewise_attn_bwd_workspace_size(int B, int H, int TQ, int TKV, int D) {
+  if (B <= 0 || H <= 0 || TQ <= 0 || TKV <= 0 || D != ICSA_D) return ICSA_EINVAL;
+  if (TQ % ICSA_BLOCK || TKV % ICSA_BLOCK) return ICSA_EINVAL;
+  return bwd_layout(B, H, TQ, TKV).total;
+}
+
+int icsa_sparse_piecewise_attn_bwd(
+    const void* dout, int64_t do_sb, int64_t do_sh, int64_t do_st,
+    const void* q, int64_t q_sb, int64_t q_sh, int64_t q_st,
+    const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st,
+    const void* v, int64_t v_sb, int64_t v_sh, int64_t v_st,
+    const void* out, int64_t o_sb, int64_t o_sh, int64_t o_st,
+    const float* lse, const int32_t* idx,
+    int B, int H, int TQ, int TKV, int D, int top_k,
+    void* dq, int dq_dtype, int64_t dq_sb, int64_t dq_sh, int64_t dq_st,
+    void* dk, int dk_dtype, int64_t dk_sb, int64_t dk_sh, int64_t dk_st,
+    void* dv, int dv_dtype, int64_t dv_sb, int64_t dv_sh, int64_t dv_st,
+    void* workspace, int64_t workspace_bytes, void* stream_) {
+  int rc = validate_common(B, TQ, H, D);
+  if (rc) return rc;
+  if ((rc = check_dtype(dq_dtype, "dq")) || (rc = check_dtype(dk_dtype, "dk")) || (rc = check_dtype(dv_dtype, "dv")))
+    return rc;
+  if (TKV <= 0) return fail(ICSA_EINVAL, "TKV must be positive");
+  if (TQ % ICSA_BLOCK || TKV % ICSA_BLOCK)
+    return fail(ICSA_EINVAL, "TQ/TKV must be divisible by the block size 64 (got %d, %d)", TQ, TKV);
+  if (!dout || !q || !k || !v || !out || !lse || !idx || !dq || !dk || !dv || !workspace)
+    return fail(ICSA_EINVAL, "null pointer argument");
+  if (!row_ok(dout, ICSA_BF16, do_sb, do_sh, do_st) || !row_ok(q, ICSA_BF16, q_sb, q_sh, q_st) ||
+      !row_ok(k, ICSA_BF16, k_sb, k_sh, k_st) || !row_ok(v, ICSA_BF16, v_sb, v_sh, v_st) ||
+      !row_ok(out, ICSA_BF16, o_sb, o_sh, o_st) || !row_ok(dq, dq_dtype, dq_sb, dq_sh, dq_st) ||
+      !row_ok(dk, dk_dtype, dk_sb, dk_sh, dk_st) || !row_ok(dv, dv_dtype, dv_sb, dv_sh, dv_st))
+    return fail(ICSA_EINVAL, "rows must be 16-byte aligned (pointer and strides)");
+  const int NQ = TQ / ICSA_BLOCK, NKV = TKV / ICSA_BLOCK;
+  if (NQ > 4096 || NKV > 2048)
+    return fail(ICSA_EUNSUPPORTED, "NQ=%d / NKV=%d exceed limits (4096 / 2048)", NQ, NKV);
+  if (top_k < 1 || top_k > 512 || top_k > NKV)
+    return fail(ICSA_EINVAL, "top_k=%d must be in [1, min(512, NKV=%d)]", top_k, NKV);
+  const BwLayout L = bwd_layout(B, H, TQ, TKV);
+  if (workspace_bytes < L.total)
+    return fail(ICSA_EWORKSPACE, "workspace %lld bytes < required %lld", (long long)workspace_bytes,
+                (long long)L.total);
+  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+  char* ws = reinterpret_cast<char*>(workspace);
+  const int nc = ceil_div(NKV, 64);
+
+  PoolParams pk;                                   // f32 block sums of k / v and K^T
+  std::memset(&pk, 0, sizeof(pk));
+  pk.x[1] = TokTensor{k, k_sb, k_st, k_sh, ICSA_BF16};
+  pk.x[2] = TokTensor{v, v_sb, v_st, v_sh, ICSA_BF16};
+  pk.sums[1] = reinterpret_cast<float*>(ws + L.ksum);
+  pk.sums[2] = reinterpret_cast<float*>(ws + L.vsum);
+  pk.vt = reinterpret_cast<bf16*>(ws + L.kt); pk.vt_src = 1;
+  pk.vt_sb = (int64_t)H * ICSA_D * TKV; pk.vt_sh = (int64_t)ICSA_D * TKV; pk.vt_sd = TKV;
+  pk.B = B; pk.S = TKV; pk.H = H; pk.NB = NKV;
+  ICSA_HIP_TRY(launch_pool(pk, stream), "pool k/v");
+  PoolParams pq;                                   // Q^T, then dO^T
+  std::memset(&pq, 0, sizeof(pq));
+  pq.x[0] = TokTensor{q, q_sb, q_st, q_sh, ICSA_BF16};
+  pq.vt = reinterpret_cast<bf16*>(ws + L.qt); pq.vt_src = 0;
+  pq.vt_sb = (int64_t)H * ICSA_D * TQ; pq.vt_sh = (int64_t)ICSA_D * TQ; pq.vt_sd = TQ;
+  pq.B = B; pq.S = TQ; pq.H = H; pq.NB = NQ;
+  ICSA_HIP_TRY(launch_pool(pq, stream), "transpose q");
+  pq.x[0] = TokTensor{dout, do_sb, do_st, do_sh, ICSA_BF16};
+  pq.vt = reinterpret_cast<bf16*>(ws + L.dot);
+  ICSA_HIP_TRY(launch_pool(pq, stream), "transpose dout");
+
+  SparseBwdParams p;
+  std::memset(&p, 0, sizeof(p));
+  p.q = reinterpret_cast<const bf16*>(q); p.q_sb = q_sb; p.q_sh = q_sh; p.q_st = q_st;
+  p.k = reinterpret_cast<const bf16*>(k); p.k_sb = k_sb; p.k_sh = k_sh; p.k_st = k_st;
+  p.v = reinterpret_cast<const bf16*>(v); p.v_sb = v_sb; p.v_sh = v_sh; p.v_st = v_st;
+  p.dout = reinterpret_cast<const bf16*>(dout); p.do_sb = do_sb; p.do_sh = do_sh; p.do_st = do_st;
+  p.out = reinterpret_cast<const bf16*>(out); p.o_sb = o_sb; p.o_sh = o_sh; p.o_st = o_st;
+  p.lse = lse; p.idx = idx;
+  p.B = B; p.H = H; p.TQ = TQ; p.TKV = TKV; p.NQ = NQ; p.NKV = NKV; p.nc = nc; p.NKVp = nc * 64;
+  p.top_k = top_k; p.nsplit = L.nsplit; p.qb_per_split = L.qb_per_split;
+  p.scale = 1.0f / std::sqrt((float)ICSA_D);
+  p.scale_log2 = kLog2e / std::sqrt((float)ICSA_D);
+  p.qt = reinterpret_cast<const bf16*>(ws + L.qt);
+  p.dot = reinterpret_cast<const bf16*>(ws + L.dot);
+  p.kt = reinterpret_cast<const bf16*>(ws + L.kt);
+  p.ksum = pk.sums[1]; p.vsum = pk.sums[2];
+  p.dvec = reinterpret_cast<float*>(ws + L.dvec);
+  p.selbits = reinterpret_cast<unsigned long long*>(ws + L.selbits);
+  p.kcb = reinterpret_cast<bf16*>(ws + L.kcb);
+  p.vcb = reinterpret_cast<bf16*>(ws + L.vcb);
+  p.kct = reinterpret_cast<bf16*>(ws + L.kct);
+  p.dkc_part = reinterpret_cast<float*>(ws + L.dkc);
+  p.dvc_part = reinterpret_cast<float*>(ws + L.dvc);
+  p.dq = OutView{dq, dq_sb, dq_st, dq_sh, dq_dtype == ICSA_F32 ? ICSA_DT_F32 : ICSA_DT_BF16};
+  p.dk = OutView{dk, dk_sb, dk_st, dk_sh, dk_dtype == ICSA_F32 ? ICSA_DT_F32 : ICSA_DT_BF16};
+  p.dv = OutView{dv, dv_sb, dv_st, dv_sh, dv_dtype == ICSA_F32 ? ICSA_DT_F32 : ICSA_DT_BF16};
+  ICSA_HIP_TRY(launch_sparse_bwd_prep(p, stream), "backward prep");
+  ICSA_HIP_TRY(launch_sparse_bwd(p, stream), "backward");
+  return ICSA_OK;
+}
 
 int64_t icsa_flash_attn_workspace_size(int B, int Sk, int H, int D) {
   if (B <= 0 || Sk <= 0 || H <= 0 || D != ICSA_D) return -1;

@@ -149,5 +149,33 @@ struct SparseParams {
   AlphaView alpha;
   OutView out;
   float scale_log2;
+  float* lse;                        // optional [BH, Sq]: m + log2(l + g_l) per query (log2 units)
 };
 hipError_t launch_sparse(const SparseParams& p, hipStream_t stream);
+
+// ---------------------------------------------------------------- backward (sparse_bwd.hip)
+// Gradients of the sparse piecewise attention (triton_kernels.py:265-486, 541-598) without
+// atomics: dq query-major, dk / dv key-major over fixed-order query lists.
+struct SparseBwdParams {
+  const bf16* q;    int64_t q_sb, q_sh, q_st;     // [B, H, TQ, D] element strides
+  const bf16* k;    int64_t k_sb, k_sh, k_st;     // [B, H, TKV, D]
+  const bf16* v;    int64_t v_sb, v_sh, v_st;
+  const bf16* dout; int64_t do_sb, do_sh, do_st;  // [B, H, TQ, D]
+  const bf16* out;  int64_t o_sb, o_sh, o_st;
+  const float* lse;                  // [BH, TQ] log2 units
+  const int* idx;                    // [BH, NQ, top_k]
+  int B, H, TQ, TKV, NQ, NKV, NKVp, nc, top_k, nsplit, qb_per_split;
+  float scale, scale_log2;
+  // workspace
+  const bf16* qt; const bf16* dot;   // [BH, D, TQ]  kv_slot order (pool kernel's transposed copy)
+  const bf16* kt;                    // [BH, D, TKV] kv_slot order
+  const float* ksum; const float* vsum;   // [BH, NKV, D] f32 block sums
+  float* dvec;                       // [BH, TQ] rowsum(dO * O)
+  unsigned long long* selbits;       // [BH, NQ, nc] selected key blocks per query block
+  bf16* kcb; bf16* vcb;              // [BH, NKVp, D] bf16 block sums, rows >= NKV zero
+  bf16* kct;                         // [BH, D, NKVp] kv_slot order
+  float* dkc_part; float* dvc_part;  // [nsplit, BH, NKVp, D] interval partials
+  OutView dq, dk, dv;                // (sb, token stride, sh, dtype)
+};
+hipError_t launch_sparse_bwd_prep(const SparseBwdParams& p, hipStream_t stream);
+hipError_t launch_sparse_bwd(const SparseBwdParams& p, hipStream_t stream);

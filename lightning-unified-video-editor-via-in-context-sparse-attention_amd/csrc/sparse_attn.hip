@@ -361,6 +361,10 @@ icsa_sparse_kernel(SparseParams p) {
   const float inv = den == 0.f ? 0.f : 1.f / den;
   float* o_lds = reinterpret_cast<float*>(wave == 0 ? kbuf : vbuf);
   stage_o(o_lds, o, inv);
+  // the log-sum-exp the Triton forward saves for its backward (triton_kernels.py:249-252):
+  // final running max + log2 of the combined denominator, in log2-scaled score units
+  if (p.lse != nullptr && hl == 0 && li < q_valid)
+    p.lse[(int64_t)bh * p.Sq + qtok0 + li] = m_run + log2f(den);
   __syncthreads();
   if (q_valid > 0) {
     const float* oc = p.out_c ? p.out_c + ((int64_t)bh * p.nb_q + qblk) * ICSA_D : nullptr;

@@ -16,7 +16,10 @@ from .hip_host import (  # noqa: F401
     flash_attn_func,
     gather_kv,
     pool,
+    SparsePiecewiseAttn1stIntervalsFunction,
     sparse_piecewise_attn_1st_intervals,
+    sparse_piecewise_attn_1st_intervals_bwd_hip,
+    sparse_piecewise_attn_1st_intervals_fwd_hip,
     sparse_piecewise_attn_1st_intervals_hip,
 )
 
@@ -26,6 +29,9 @@ __all__ = [
     'editing_sparse_attention_tilelang',
     'sparse_piecewise_attn_1st_intervals_hip',
     'sparse_piecewise_attn_1st_intervals',
+    'SparsePiecewiseAttn1stIntervalsFunction',
+    'sparse_piecewise_attn_1st_intervals_fwd_hip',
+    'sparse_piecewise_attn_1st_intervals_bwd_hip',
     'flash_attn_func',
     'derived_sizes',
     'IcsaArgumentError',

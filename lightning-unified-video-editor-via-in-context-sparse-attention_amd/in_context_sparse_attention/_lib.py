@@ -41,7 +41,8 @@ EXPORTS = [
     "icsa_sparse_piecewise_attn", "icsa_flash_attn_workspace_size", "icsa_flash_attn",
     "icsa_pool", "icsa_gather_kv", "icsa_wan_qk_workspace_size", "icsa_wan_qk_prologue",
     "icsa_editing_sparse_attention_presummed", "icsa_wan_ln_modulate", "icsa_last_error",
-    "icsa_version",
+    "icsa_version", "icsa_sparse_piecewise_attn_fwd", "icsa_sparse_piecewise_attn_bwd_workspace_size",
+    "icsa_sparse_piecewise_attn_bwd",
 ]
 
 _p = ctypes.c_void_p
@@ -80,6 +81,27 @@ _SIGNATURES = {
         _i, _i, _i, _i, _i, _d,
         _p, _p,
         _p, _l, _l, _l,
+        _p, _l, _p]),
+    "icsa_sparse_piecewise_attn_fwd": (_i, [
+        _p, _l, _l, _l,
+        _p, _l, _l, _l,
+        _p, _l, _l, _l,
+        _i, _i, _i, _i, _i, _d,
+        _p, _p,
+        _p, _l, _l, _l, _p,
+        _p, _l, _p]),
+    "icsa_sparse_piecewise_attn_bwd_workspace_size": (_l, [_i, _i, _i, _i, _i]),
+    "icsa_sparse_piecewise_attn_bwd": (_i, [
+        _p, _l, _l, _l,
+        _p, _l, _l, _l,
+        _p, _l, _l, _l,
+        _p, _l, _l, _l,
+        _p, _l, _l, _l,
+        _p, _p,
+        _i, _i, _i, _i, _i, _i,
+        _p, _i, _l, _l, _l,
+        _p, _i, _l, _l, _l,
+        _p, _i, _l, _l, _l,
         _p, _l, _p]),
     "icsa_flash_attn_workspace_size": (_l, [_i, _i, _i, _i]),
     "icsa_flash_attn": (_i, [

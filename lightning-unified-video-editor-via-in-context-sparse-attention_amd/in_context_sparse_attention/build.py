@@ -18,8 +18,8 @@ CSRC_DIR = os.path.join(os.path.dirname(PKG_DIR), "csrc")
 BUILD_DIR = os.path.join(CSRC_DIR, "_build")
 LIB_PATH = os.path.join(PKG_DIR, "libicsa.so")
 
-SOURCES = ["pool.hip", "compressed.hip", "gather.hip", "flash_attn.hip", "sparse_attn.hip", "wan_qk.hip",
-           "wan_block.hip", "api.hip"]
+SOURCES = ["pool.hip", "compressed.hip", "gather.hip", "flash_attn.hip", "sparse_attn.hip", "sparse_bwd.hip",
+           "wan_qk.hip", "wan_block.hip", "api.hip"]
 
 HIP_FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",

@@ -118,6 +118,125 @@ def sparse_piecewise_attn_1st_intervals_hip(q: torch.Tensor, k: torch.Tensor, v:
 sparse_piecewise_attn_1st_intervals = sparse_piecewise_attn_1st_intervals_hip
 
 
+def _check_sparse_args(q, k, v, block_size):
+    """The TileLang host's argument checks (tilelang_host.py:251-259)."""
+    _require(q.dtype == k.dtype == v.dtype == torch.bfloat16, "q, k, v must be bfloat16")
+    _require(q.is_cuda and k.is_cuda and v.is_cuda, "q, k, v must be on the GPU")
+    _require(block_size == 64, "Only block_size=64 supported.")
+    _require(q.ndim == 4 and k.ndim == 4 and v.ndim == 4, "q, k, v must be 4-D [B, H, T, D]")
+    _require(q.shape[0] == k.shape[0] == v.shape[0], "batch mismatch")
+    _require(q.shape[1] == k.shape[1] == v.shape[1], "head mismatch")
+    _require(q.shape[3] == k.shape[3], "Kdim must match between q and k")
+    _require(k.shape[2] == v.shape[2], "TKV must match between k and v")
+    _require(v.shape[3] == q.shape[3], "This entrypoint assumes Vdim == D (so VBlocks==1).")
+    _require(q.shape[2] % BLOCK_M == 0 and k.shape[2] % BLOCK_M == 0, "TQ/TKV must be divisible by BT")
+
+
+@torch.no_grad()
+def sparse_piecewise_attn_1st_intervals_fwd_hip(q, k, v, sparsity: float = 0.1, block_size: int = 64,
+                                                indices: torch.Tensor = None):
+    """The forward of SparsePiecewiseAttn1stIntervalsFunction (triton_kernels.py:489-539)
+    with the state its backward needs.  Returns ``(out, lse, indices)``: out bf16
+    [B, H, TQ, D]; lse f32 [B, H, TQ] in log2 units (the final running max of the
+    log2-scaled scores plus log2 of the combined denominator); indices int32
+    [B, H, TQ/64, top_k] (``indices`` given: used instead of the kernel's own top-k)."""
+    _check_sparse_args(q, k, v, block_size)
+    B, H, TQ, D = q.shape
+    TKV = k.shape[2]
+    q, k, v = inner_contiguous(q), inner_contiguous(k), inner_contiguous(v)
+    L = _lib.lib()
+    NQ, NKV = TQ // BLOCK_M, TKV // BLOCK_M
+    top_k = max(1, int(sparsity * NKV))
+    out = torch.empty(B, H, TQ, D, dtype=torch.bfloat16, device=q.device)
+    lse = torch.empty(B, H, TQ, dtype=torch.float32, device=q.device)
+    idx = torch.empty(B, H, NQ, top_k, dtype=torch.int32, device=q.device)
+    ws_bytes = L.icsa_sparse_piecewise_workspace_size(B, H, TQ, TKV, D, float(sparsity))
+    if ws_bytes < 0:
+        raise _lib.IcsaError("icsa_sparse_piecewise_workspace_size", int(ws_bytes))
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
+    inj = None
+    if indices is not None:
+        inj = indices.to(device=q.device, dtype=torch.int32).contiguous()
+        _require(tuple(inj.shape) == (B, H, NQ, top_k), f"indices must be [B, H, {NQ}, {top_k}]")
+    rc = L.icsa_sparse_piecewise_attn_fwd(
+        ptr(q), q.stride(0), q.stride(1), q.stride(2),
+        ptr(k), k.stride(0), k.stride(1), k.stride(2),
+        ptr(v), v.stride(0), v.stride(1), v.stride(2),
+        B, H, TQ, TKV, D, float(sparsity),
+        ptr(inj), ptr(idx),
+        ptr(out), out.stride(0), out.stride(1), out.stride(2), ptr(lse),
+        ptr(ws), ws_bytes, stream_ptr(q.device))
+    _lib.check("icsa_sparse_piecewise_attn_fwd", rc)
+    return out, lse, idx
+
+
+@torch.no_grad()
+def sparse_piecewise_attn_1st_intervals_bwd_hip(do, q, k, v, out, lse, indices, grad_dtype=None):
+    """Gradients ``(dq, dk, dv)`` of the sparse piecewise attention, as
+    SparsePiecewiseAttn1stIntervalsFunction.backward (triton_kernels.py:541-598) computes
+    them from the saved (q, k, v, out, lse, indices), without atomics (the same inputs give
+    the same bits).  ``grad_dtype``: bf16 (default: q.dtype, as the reference's final cast)
+    or float32."""
+    _check_sparse_args(q, k, v, 64)
+    B, H, TQ, D = q.shape
+    TKV = k.shape[2]
+    NQ = TQ // BLOCK_M
+    _require(do.shape == q.shape and out.shape == q.shape, "do / out must be [B, H, TQ, D] like q")
+    _require(do.dtype == torch.bfloat16 and out.dtype == torch.bfloat16, "do / out must be bfloat16")
+    _require(tuple(lse.shape) == (B, H, TQ) and lse.dtype == torch.float32, "lse must be f32 [B, H, TQ]")
+    _require(indices.dim() == 4 and tuple(indices.shape[:3]) == (B, H, NQ),
+             f"indices must be [B, H, {NQ}, top_k]")
+    gd = q.dtype if grad_dtype is None else grad_dtype
+    _require(gd in (torch.bfloat16, torch.float32), "grad_dtype must be bfloat16 or float32")
+    q, k, v, do, out = (inner_contiguous(t) for t in (q, k, v, do, out))
+    lse = lse.contiguous()
+    idx = indices.to(dtype=torch.int32).contiguous()
+    top_k = idx.shape[-1]
+    L = _lib.lib()
+    dq = torch.empty(B, H, TQ, D, dtype=gd, device=q.device)
+    dk = torch.empty(B, H, TKV, D, dtype=gd, device=q.device)
+    dv = torch.empty(B, H, TKV, D, dtype=gd, device=q.device)
+    ws_bytes = L.icsa_sparse_piecewise_attn_bwd_workspace_size(B, H, TQ, TKV, D)
+    if ws_bytes < 0:
+        raise _lib.IcsaError("icsa_sparse_piecewise_attn_bwd_workspace_size", int(ws_bytes))
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
+    g = dtype_code(dq)
+    rc = L.icsa_sparse_piecewise_attn_bwd(
+        ptr(do), do.stride(0), do.stride(1), do.stride(2),
+        ptr(q), q.stride(0), q.stride(1), q.stride(2),
+        ptr(k), k.stride(0), k.stride(1), k.stride(2),
+        ptr(v), v.stride(0), v.stride(1), v.stride(2),
+        ptr(out), out.stride(0), out.stride(1), out.stride(2),
+        ptr(lse), ptr(idx),
+        B, H, TQ, TKV, D, top_k,
+        ptr(dq), g, dq.stride(0), dq.stride(1), dq.stride(2),
+        ptr(dk), g, dk.stride(0), dk.stride(1), dk.stride(2),
+        ptr(dv), g, dv.stride(0), dv.stride(1), dv.stride(2),
+        ptr(ws), ws_bytes, stream_ptr(q.device))
+    _lib.check("icsa_sparse_piecewise_attn_bwd", rc)
+    return dq, dk, dv
+
+
+class SparsePiecewiseAttn1stIntervalsFunction(torch.autograd.Function):
+    """Autograd function of the sparse piecewise attention on MI355X, with the reference
+    Function's interface (triton_kernels.py:489-598): ``apply(q, k, v, sparsity,
+    block_size)``; the backward returns (dq, dk, dv) in the inputs' dtype and None for
+    sparsity and block_size."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, sparsity, block_size):
+        out, lse, idx = sparse_piecewise_attn_1st_intervals_fwd_hip(q, k, v, sparsity, block_size)
+        ctx.save_for_backward(q, k, v, out, lse, idx)
+        return out
+
+    @staticmethod
+    def backward(ctx, do):
+        q, k, v, out, lse, idx = ctx.saved_tensors
+        dq, dk, dv = sparse_piecewise_attn_1st_intervals_bwd_hip(
+            do.to(torch.bfloat16), q, k, v, out, lse, idx)
+        return dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), None, None
+
+
 @torch.no_grad()
 def flash_attn_func(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, dropout_p: float = 0.0,
                     softmax_scale=None, causal: bool = False, out_dtype=None) -> torch.Tensor:

@@ -281,7 +281,7 @@ def dense_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
 
 def sparse_piecewise_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                           sparsity: float = 0.1, indices: Optional[torch.Tensor] = None,
-                          dtype=torch.float64, qchunk: int = 64):
+                          dtype=torch.float64, qchunk: int = 64, return_lse: bool = False):
     """Sparse piecewise attention with the first-order interval approximation.
 
     Semantics of ``sparse_piecewise_attn_1st_intervals_tilelang`` (tilelang_host.py:229-274
@@ -300,7 +300,10 @@ def sparse_piecewise_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
       ``g_l`` (``+= p VC``, ``+= 64 sum p``) are *not* rescaled when the max grows later.
     * ``out = (acc + g_acc) / (l + g_l)``, 0 where the denominator is 0 (:980-992).
 
-    Returns ``(out [B,H,TQ,D], indices [B,H,NQ,top_k] ascending, scores [B,H,NQ,NKV])``.
+    Returns ``(out [B,H,TQ,D], indices [B,H,NQ,top_k] ascending, scores [B,H,NQ,NKV])``,
+    and with ``return_lse`` also ``lse [B,H,TQ]`` as the Triton forward stores it for the
+    backward (triton_kernels.py:249-252): ``m + log2(l + g_l)`` in log2 units (the final
+    running max of the log2-scaled scores; ``-inf`` where the denominator is 0).
     """
     B, H, TQ, D = q.shape
     TKV = k.shape[2]
@@ -321,6 +324,7 @@ def sparse_piecewise_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     kb = kd.view(B, H, NKV, BLOCK_M, D)
     vb = vd.view(B, H, NKV, BLOCK_M, D)
     out = torch.empty(B, H, TQ, D, dtype=dtype)
+    lse = torch.empty(B, H, TQ, dtype=dtype)
     bi = torch.arange(B).view(B, 1, 1, 1)
     hi = torch.arange(H).view(1, H, 1, 1)
     for n0 in range(0, NQ, qchunk):
@@ -355,6 +359,10 @@ def sparse_piecewise_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         o = (acc + g_acc) / torch.where(den == 0, torch.ones_like(den), den)[..., None]
         o = torch.where((den == 0)[..., None], torch.zeros_like(o), o)
         out[:, :, n0 * BLOCK_M:n1 * BLOCK_M] = o.reshape(B, H, (n1 - n0) * BLOCK_M, D)
+        lse[:, :, n0 * BLOCK_M:n1 * BLOCK_M] = ((m + torch.log(den)) / math.log(2.0)).reshape(
+            B, H, (n1 - n0) * BLOCK_M)
+    if return_lse:
+        return out, indices, scores, lse
     return out, indices, scores
 
 
