@@ -370,6 +370,65 @@ def dit_step_bench(steps, log_fn):
     return res
 
 
+def sparse_bwd_bench(steps, warmup, log_fn):
+    """The sparse kernel's forward (with the saved state) and backward at configuration 2's
+    sparse-stage shape: B=1, H=40, the 32,768 diffuse queries (512 blocks) against the new
+    KV of 36,864 tokens (576 blocks), top_k = int(0.0625 * 576) = 36.  Algorithmic FLOPs of
+    the backward are the reference kernel's five 64-row matmuls per exact block and per
+    interval chunk (triton_kernels.py:330-475): BH * NQ * (top_k * 5 * 2*64*64*128 +
+    5 * 2*64*NKVp*128)."""
+    import torch
+    from in_context_sparse_attention import (sparse_piecewise_attn_1st_intervals_bwd_hip,
+                                             sparse_piecewise_attn_1st_intervals_fwd_hip)
+    dev = torch.device("cuda:0")
+    B, H, TQ, TKV, D, sar = 1, 40, 32768, 36864, 128, 0.0625
+    g = torch.Generator(device=dev).manual_seed(0)
+    q = torch.randn(B, H, TQ, D, device=dev, generator=g).to(torch.bfloat16)
+    k = torch.randn(B, H, TKV, D, device=dev, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, H, TKV, D, device=dev, generator=g).to(torch.bfloat16)
+    do = torch.randn(B, H, TQ, D, device=dev, generator=g).to(torch.bfloat16)
+    NQ, NKV = TQ // 64, TKV // 64
+    NKVp = (NKV + 63) // 64 * 64
+    top_k = max(1, int(sar * NKV))
+    stream = torch.cuda.current_stream(dev)
+
+    def timed(fn, n):
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+        for a, b in ev:
+            a.record(stream)
+            fn()
+            b.record(stream)
+        torch.cuda.synchronize()
+        return statistics.median(a.elapsed_time(b) for a, b in ev)
+
+    state = {}
+
+    def fwd():
+        state["f"] = sparse_piecewise_attn_1st_intervals_fwd_hip(q, k, v, sar)
+
+    def bwd():
+        out, lse, idx = state["f"]
+        sparse_piecewise_attn_1st_intervals_bwd_hip(do, q, k, v, out, lse, idx)
+
+    for _ in range(max(1, warmup)):
+        fwd()
+        bwd()
+    torch.cuda.synchronize()
+    n = max(3, steps)
+    fwd_ms = timed(fwd, n)
+    bwd_ms = timed(bwd, n)
+    BH = B * H
+    flops = BH * NQ * (top_k * 5 * 2.0 * 64 * 64 * D + 5 * 2.0 * 64 * NKVp * D)
+    res = {"fwd_ms": fwd_ms, "bwd_ms": bwd_ms, "bwd_tflop": flops / 1e12,
+           "bwd_tflops": flops / (bwd_ms * 1e-3) / 1e12,
+           "bwd_mfma_frac": flops / (bwd_ms * 1e-3) / 2.5e15,
+           "workload": (f"sparse kernel at configuration 2's sparse stage: B={B} H={H} TQ={TQ} "
+                        f"TKV={TKV} top_k={top_k}, bf16 N(0,1) q / k / v / dout")}
+    log_fn(f"[bench] sparse backward (cfg 2 sparse stage): forward {fwd_ms:.2f} ms, backward "
+           f"{bwd_ms:.2f} ms = {res['bwd_tflops']:.0f} TFLOP/s on {flops / 1e12:.2f} TFLOP")
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -392,6 +451,9 @@ def main():
                     help="skip the configuration-4 DiT block leg")
     ap.add_argument("--block-only", action="store_true",
                     help="run only the configuration-4 DiT block leg (for profiling)")
+    ap.add_argument("--sparse-bwd", action="store_true",
+                    help="run only the sparse kernel's forward + backward at configuration 2's "
+                         "sparse-stage shape")
     ap.add_argument("--dit-step", action="store_true",
                     help="run only configuration 5: one CFG denoising step of the 40-block DiT "
                          "(several seconds per step; --steps timed steps after one warmup)")
@@ -416,6 +478,9 @@ def main():
     _lib.lib()
     if args.wan_only:
         print(json.dumps({"wan_attention": wan_attention_bench(args.steps, args.warmup, log)}), flush=True)
+        return
+    if args.sparse_bwd:
+        print(json.dumps({"sparse_bwd": sparse_bwd_bench(args.steps, args.warmup, log)}), flush=True)
         return
     if args.dit_step:
         print(json.dumps({"dit_step": dit_step_bench(max(1, args.steps), log)}), flush=True)
