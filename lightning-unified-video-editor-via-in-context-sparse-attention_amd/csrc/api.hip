@@ -685,11 +685,12 @@ int icsa_sparse_piecewise_attn_fwd(
 
 namespace {
 struct BwLayout {
-  int64_t ksum, vsum, kt, qt, dot, dvec, selbits, kcb, vcb, kct, dkc, dvc, total;
+  int64_t ksum, vsum, dvec, selbits, kcb, vcb, dkc, dvc, total;
   int nsplit, qb_per_split;
 };
 // Interval partials: enough (chunk, query-range) workgroups to fill the GPU, each range at
-// least 8 query blocks long.
+// least 8 and at most 1024 query blocks long (the kernel stages a range's selection words
+// in LDS).
 BwLayout bwd_layout(int B, int H, int TQ, int TKV) {
   const int64_t BH = (int64_t)B * H;
   const int NQ = TQ / ICSA_BLOCK, NKV = TKV / ICSA_BLOCK;
@@ -697,20 +698,16 @@ BwLayout bwd_layout(int B, int H, int TQ, int TKV) {
   BwLayout L;
   const int want = std::max(1, ceil_div(1024, (int)std::max<int64_t>(1, BH * nc)));
   int qbps = std::max(8, ceil_div(NQ, want));
-  qbps = std::min(qbps, NQ);
+  qbps = std::min(qbps, std::min(NQ, 1024));
   L.qb_per_split = qbps;
   L.nsplit = ceil_div(NQ, qbps);
   int64_t o = 0;
   L.ksum = o; o += align256(BH * NKV * ICSA_D * 4);
   L.vsum = o; o += align256(BH * NKV * ICSA_D * 4);
-  L.kt = o; o += align256(BH * ICSA_D * (int64_t)TKV * 2);
-  L.qt = o; o += align256(BH * ICSA_D * (int64_t)TQ * 2);
-  L.dot = o; o += align256(BH * ICSA_D * (int64_t)TQ * 2);
   L.dvec = o; o += align256(BH * (int64_t)TQ * 4);
   L.selbits = o; o += align256(BH * NQ * (int64_t)nc * 8);
   L.kcb = o; o += align256(BH * NKVp * ICSA_D * 2);
   L.vcb = o; o += align256(BH * NKVp * ICSA_D * 2);
-  L.kct = o; o += align256(BH * ICSA_D * NKVp * 2);
   L.dkc = o; o += align256((int64_t)L.nsplit * BH * NKVp * ICSA_D * 4);
   L.dvc = o; o += align256((int64_t)L.nsplit * BH * NKVp * ICSA_D * 4);
   L.total = o;
@@ -765,26 +762,14 @@ int icsa_sparse_piecewise_attn_bwd(
   char* ws = reinterpret_cast<char*>(workspace);
   const int nc = ceil_div(NKV, 64);
 
-  PoolParams pk;                                   // f32 block sums of k / v and K^T
+  PoolParams pk;                                   // f32 block sums of k / v (the forward's)
   std::memset(&pk, 0, sizeof(pk));
   pk.x[1] = TokTensor{k, k_sb, k_st, k_sh, ICSA_BF16};
   pk.x[2] = TokTensor{v, v_sb, v_st, v_sh, ICSA_BF16};
   pk.sums[1] = reinterpret_cast<float*>(ws + L.ksum);
   pk.sums[2] = reinterpret_cast<float*>(ws + L.vsum);
-  pk.vt = reinterpret_cast<bf16*>(ws + L.kt); pk.vt_src = 1;
-  pk.vt_sb = (int64_t)H * ICSA_D * TKV; pk.vt_sh = (int64_t)ICSA_D * TKV; pk.vt_sd = TKV;
   pk.B = B; pk.S = TKV; pk.H = H; pk.NB = NKV;
   ICSA_HIP_TRY(launch_pool(pk, stream), "pool k/v");
-  PoolParams pq;                                   // Q^T, then dO^T
-  std::memset(&pq, 0, sizeof(pq));
-  pq.x[0] = TokTensor{q, q_sb, q_st, q_sh, ICSA_BF16};
-  pq.vt = reinterpret_cast<bf16*>(ws + L.qt); pq.vt_src = 0;
-  pq.vt_sb = (int64_t)H * ICSA_D * TQ; pq.vt_sh = (int64_t)ICSA_D * TQ; pq.vt_sd = TQ;
-  pq.B = B; pq.S = TQ; pq.H = H; pq.NB = NQ;
-  ICSA_HIP_TRY(launch_pool(pq, stream), "transpose q");
-  pq.x[0] = TokTensor{dout, do_sb, do_st, do_sh, ICSA_BF16};
-  pq.vt = reinterpret_cast<bf16*>(ws + L.dot);
-  ICSA_HIP_TRY(launch_pool(pq, stream), "transpose dout");
 
   SparseBwdParams p;
   std::memset(&p, 0, sizeof(p));
@@ -798,15 +783,11 @@ int icsa_sparse_piecewise_attn_bwd(
   p.top_k = top_k; p.nsplit = L.nsplit; p.qb_per_split = L.qb_per_split;
   p.scale = 1.0f / std::sqrt((float)ICSA_D);
   p.scale_log2 = kLog2e / std::sqrt((float)ICSA_D);
-  p.qt = reinterpret_cast<const bf16*>(ws + L.qt);
-  p.dot = reinterpret_cast<const bf16*>(ws + L.dot);
-  p.kt = reinterpret_cast<const bf16*>(ws + L.kt);
   p.ksum = pk.sums[1]; p.vsum = pk.sums[2];
   p.dvec = reinterpret_cast<float*>(ws + L.dvec);
   p.selbits = reinterpret_cast<unsigned long long*>(ws + L.selbits);
   p.kcb = reinterpret_cast<bf16*>(ws + L.kcb);
   p.vcb = reinterpret_cast<bf16*>(ws + L.vcb);
-  p.kct = reinterpret_cast<bf16*>(ws + L.kct);
   p.dkc_part = reinterpret_cast<float*>(ws + L.dkc);
   p.dvc_part = reinterpret_cast<float*>(ws + L.dvc);
   p.dq = OutView{dq, dq_sb, dq_st, dq_sh, dq_dtype == ICSA_F32 ? ICSA_DT_F32 : ICSA_DT_BF16};

@@ -167,13 +167,10 @@ struct SparseBwdParams {
   int B, H, TQ, TKV, NQ, NKV, NKVp, nc, top_k, nsplit, qb_per_split;
   float scale, scale_log2;
   // workspace
-  const bf16* qt; const bf16* dot;   // [BH, D, TQ]  kv_slot order (pool kernel's transposed copy)
-  const bf16* kt;                    // [BH, D, TKV] kv_slot order
   const float* ksum; const float* vsum;   // [BH, NKV, D] f32 block sums
   float* dvec;                       // [BH, TQ] rowsum(dO * O)
   unsigned long long* selbits;       // [BH, NQ, nc] selected key blocks per query block
   bf16* kcb; bf16* vcb;              // [BH, NKVp, D] bf16 block sums, rows >= NKV zero
-  bf16* kct;                         // [BH, D, NKVp] kv_slot order
   float* dkc_part; float* dvc_part;  // [nsplit, BH, NKVp, D] interval partials
   OutView dq, dk, dv;                // (sb, token stride, sh, dtype)
 };

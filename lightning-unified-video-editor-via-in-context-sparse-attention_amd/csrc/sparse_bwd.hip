@@ -35,29 +35,6 @@
 #define BW_MAX_NQ 4096
 #define BW_STAGE_BYTES (32 * O_LDS_STRIDE * 4)   // one wave's fp32 staging rows
 
-// 64 x 128 bf16 row tile (rows at src, row stride rs elements) -> LDS, XOR-swizzled as a K tile.
-__device__ __forceinline__ void bw_row_tile(bf16* dst, const bf16* src, int64_t rs) {
-  const int t = threadIdx.x;
-  const int c = t & 15;
-  u32x4 r[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) r[i] = *reinterpret_cast<const u32x4*>(src + (int64_t)((t >> 4) + 8 * i) * rs + 8 * c);
-#pragma unroll
-  for (int i = 0; i < 8; ++i) *reinterpret_cast<u32x4*>(dst + k_lds_off((t >> 4) + 8 * i, c)) = r[i];
-}
-
-// [128 d][64 slots] bf16 transposed tile (d rows at src, d stride ds elements) -> LDS,
-// XOR-swizzled as a V^T tile.
-__device__ __forceinline__ void bw_t_tile(bf16* dst, const bf16* src, int64_t ds) {
-  const int t = threadIdx.x;
-  const int c = t & 7;
-  u32x4 r[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) r[i] = *reinterpret_cast<const u32x4*>(src + (int64_t)((t >> 3) + 16 * i) * ds + 8 * c);
-#pragma unroll
-  for (int i = 0; i < 8; ++i) *reinterpret_cast<u32x4*>(dst + v_lds_off((t >> 3) + 16 * i, c)) = r[i];
-}
-
 // ------------------------------------------------------------------------------------------
 // prep: D = rowsum(dO * O) per query row and the selection bitmap of each query block
 // ------------------------------------------------------------------------------------------
@@ -92,9 +69,8 @@ __global__ void __launch_bounds__(256) icsa_sparse_bwd_rows_kernel(SparseBwdPara
   if (t < p.nc) p.selbits[((int64_t)bh * p.NQ + i) * p.nc + t] = sel[t];
 }
 
-// prep: bf16 block sums (rows, and transposed in kv_slot order) from the f32 sums
+// prep: bf16 block sums from the f32 sums (rows >= NKV zero)
 __global__ void __launch_bounds__(256) icsa_sparse_bwd_sums_kernel(SparseBwdParams p) {
-  __shared__ bf16 tile[ICSA_BLOCK][ICSA_D + 8];
   const int ch = blockIdx.x, bh = blockIdx.y;
   const int t = threadIdx.x;
   const int r = t >> 2, qq = t & 3;
@@ -112,33 +88,85 @@ __global__ void __launch_bounds__(256) icsa_sparse_bwd_sums_kernel(SparseBwdPara
 #pragma unroll
         for (int e = 0; e < 8; ++e) v[e] = 0.f;
       }
-      const bf16x8 o = pack8_bf16(v);
-      *reinterpret_cast<bf16x8*>(dst + 8 * g) = o;
-      if (part == 0) *reinterpret_cast<bf16x8*>(&tile[r][32 * qq + 8 * g]) = o;
+      *reinterpret_cast<bf16x8*>(dst + 8 * g) = pack8_bf16(v);
     }
-  }
-  __syncthreads();
-  const int d = t >> 1, half = t & 1;
-  bf16* dst = p.kct + ((int64_t)bh * ICSA_D + d) * p.NKVp + (int64_t)ch * ICSA_BLOCK + 32 * half;
-#pragma unroll
-  for (int q4 = 0; q4 < 4; ++q4) {
-    bf16x8 o;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) o[e] = tile[kv_slot(32 * half + 8 * q4 + e)][d];
-    *reinterpret_cast<bf16x8*>(dst + 8 * q4) = o;
   }
 }
 
 // ------------------------------------------------------------------------------------------
-// dq: one workgroup per query block
+// Tile DMA.  A 16 KB row tile (64 rows x 128 dims, the K-tile layout of the forward) is 16
+// LDS-DMA instructions, 8 per wave; each lands 1 KB at consecutive LDS addresses (lane l
+// at +16 l), so the XOR swizzle is applied on the global side.  Loads complete in issue
+// order: with the next step's tiles in flight a kernel waits with vmcnt(their count).
 // ------------------------------------------------------------------------------------------
+#define BW_WAIT(n) asm volatile("s_waitcnt vmcnt(" #n ")" ::: "memory")
+
+__device__ __forceinline__ void bw_dma_rows(unsigned char* tile, const bf16* base, int64_t rs, int wave,
+                                            int lane) {
+  const __amdgpu_buffer_rsrc_t rsrc = make_rsrc(base, ((int64_t)(ICSA_BLOCK - 1) * rs + ICSA_D) * 2);
+  unsigned char* dst = tile + wave * 8192;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int r = 32 * wave + 4 * i + (lane >> 4);
+    const int off = (int)(r * rs * 2) + (((lane & 15) ^ (r & 15)) << 4);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_ptr)(dst + 1024 * i), 16, off, 0, 0, 0);
+  }
+}
+
+// ------------------------------------------------------------------------------------------
+// Transposed MFMA operands straight from a row tile (ds_read_b64_tr_b16).  Within each
+// group of 16 lanes, lane j of the transposing read receives element j % 4 of the 4-element
+// vectors read by lanes j / 4 + 4 e (e = 0..3).  For the A operand of
+// O^T[d][key] += X^T[d][row] P[row][key] (X a 64 x 128 row tile, lane l = 16 g + s holding
+// A[d = 32 ds + l % 32][k = 8 (l / 32) + e]) with the row order of the score accumulators
+// (k -> row 16 m + 8 (e / 4) + 4 (l / 32) + e % 4), lane 16 g + s reads the 4 dims
+// 32 ds + 16 (g % 2) + 4 (s % 4) .. + 3 of row 16 m + 4 (g / 2) + s / 4 (+ 8 for e >= 4).
+// tro[h][ds]: those byte offsets in the K-tile layout for m = 0; step m adds 16 rows.
+// ------------------------------------------------------------------------------------------
+typedef short bw_v4s __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) bw_v4s* bw_lds_v4s;
+
+__device__ __forceinline__ void tr_offsets(int tro[2][4], int lane) {
+  const int g = lane >> 4, s = lane & 15;
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int ds = 0; ds < 4; ++ds) {
+      const int row = 4 * (g >> 1) + (s >> 2) + 8 * h;
+      const int col = 32 * ds + 16 * (g & 1) + 4 * (s & 3);
+      tro[h][ds] = row * (ICSA_D * 2) + ((((col >> 3) ^ (row & 15))) << 4) + (col & 7) * 2;
+    }
+}
+
+// o[4 d-subtiles] += X^T P for a row tile X (bytes at `tile`); p[m]: bf16 B operand of
+// 16-row step m, straight from the score accumulators.
+__device__ __forceinline__ void pv_tile_tr(floatx16 o[4], const unsigned char* tile, const int tro[2][4],
+                                           const bf16x8 p[4]) {
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+#pragma unroll
+    for (int ds = 0; ds < 4; ++ds) {
+      const bw_v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((bw_lds_v4s)(tile + tro[0][ds] + m * 16 * ICSA_D * 2));
+      const bw_v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((bw_lds_v4s)(tile + tro[1][ds] + m * 16 * ICSA_D * 2));
+      const short __attribute__((ext_vector_type(8))) a8 = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      o[ds] = mfma32x32x16(__builtin_bit_cast(bf16x8, a8), p[m], o[ds]);
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------------
+// dq: one workgroup per query block.  Steps t = 0 .. n_ex + nc - 1: the valid selected
+// blocks, then the interval chunks.  Per step the K and V rows (16 DMA per wave) land in
+// one of two buffers while the other step's S^T = K Q^T, dP^T = V dO^T and
+// dQ^T += K^T dS^T (K^T read transposed from the K rows) run.
+// ------------------------------------------------------------------------------------------
+#define BWQ_LDS_BYTES (4 * K_TILE_BYTES + BW_MAX_TOPK * 4 + BW_MAX_CHUNKS * 8 + 16)
+
 __global__ void __launch_bounds__(BW_THREADS) icsa_sparse_bwd_dq_kernel(SparseBwdParams p) {
-  __shared__ __attribute__((aligned(16))) unsigned char smem[3 * K_TILE_BYTES];
-  __shared__ int src_l[BW_MAX_TOPK];
-  __shared__ unsigned long long sel_l[BW_MAX_CHUNKS];
-  bf16* ks = reinterpret_cast<bf16*>(smem);
-  bf16* vs = reinterpret_cast<bf16*>(smem + K_TILE_BYTES);
-  bf16* kts = reinterpret_cast<bf16*>(smem + 2 * K_TILE_BYTES);
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem_q[];
+  int* src_l = reinterpret_cast<int*>(smem_q + 4 * K_TILE_BYTES);
+  unsigned long long* sel_l = reinterpret_cast<unsigned long long*>(src_l + BW_MAX_TOPK);
+  int* n_ex_l = reinterpret_cast<int*>(sel_l + BW_MAX_CHUNKS);
 
   const int n_work = p.B * p.H * p.NQ;
   const int work = xcd_remap(blockIdx.x, n_work);
@@ -151,71 +179,93 @@ __global__ void __launch_bounds__(BW_THREADS) icsa_sparse_bwd_dq_kernel(SparseBw
   const int qtok0 = qb * ICSA_BLOCK + 32 * wave;
 
   for (int c = tid; c < p.nc; c += BW_THREADS) sel_l[c] = p.selbits[((int64_t)bh * p.NQ + qb) * p.nc + c];
-  for (int u = tid; u < p.top_k; u += BW_THREADS) {
-    const int j = p.idx[((int64_t)bh * p.NQ + qb) * p.top_k + u];
-    src_l[u] = (j >= 0 && j < p.NKV) ? j : -1;    // out-of-range entries: zero blocks, no gradient
+  if (wave == 0) {                                     // valid selected blocks, list order kept
+    const int* row = p.idx + ((int64_t)bh * p.NQ + qb) * p.top_k;
+    int cnt = 0;
+    for (int base = 0; base < p.top_k; base += 64) {
+      const int u = base + lane;
+      const int j = u < p.top_k ? row[u] : -1;
+      const bool on = j >= 0 && j < p.NKV;            // out-of-range entries: zero blocks, no gradient
+      const unsigned long long bal = __ballot(on);
+      if (on) src_l[cnt + __popcll(bal & ((1ull << lane) - 1ull))] = j;
+      cnt += __popcll(bal);
+    }
+    if (lane == 0) *n_ex_l = cnt;
   }
   bf16x8 qf[8], dof[8];
   load_q_frags(qf, p.q + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh + (int64_t)qtok0 * p.q_st, p.q_st, 32);
   load_q_frags(dof, p.dout + (int64_t)b * p.do_sb + (int64_t)h * p.do_sh + (int64_t)qtok0 * p.do_st, p.do_st, 32);
   const float lse = p.lse[(int64_t)bh * p.TQ + qtok0 + li];
   const float dd = p.dvec[(int64_t)bh * p.TQ + qtok0 + li];
+  int tro[2][4];
+  tr_offsets(tro, lane);
   __syncthreads();
+  const int n_ex = *n_ex_l;
+  const int T = n_ex + p.nc;
 
   const bf16* kb = p.k + (int64_t)b * p.k_sb + (int64_t)h * p.k_sh;
   const bf16* vb = p.v + (int64_t)b * p.v_sb + (int64_t)h * p.v_sh;
-  const bf16* ktb = p.kt + (int64_t)bh * ICSA_D * p.TKV;
+  const bf16* kcb = p.kcb + (int64_t)bh * p.NKVp * ICSA_D;
+  const bf16* vcb = p.vcb + (int64_t)bh * p.NKVp * ICSA_D;
+  // buffer u: K rows at 2 u tiles, V rows at 2 u + 1
+  auto issue = [&](int t) {
+    unsigned char* kt = smem_q + (t & 1) * 2 * K_TILE_BYTES;
+    if (t < n_ex) {
+      const int j = __builtin_amdgcn_readfirstlane(src_l[t]);
+      bw_dma_rows(kt, kb + (int64_t)j * ICSA_BLOCK * p.k_st, p.k_st, wave, lane);
+      bw_dma_rows(kt + K_TILE_BYTES, vb + (int64_t)j * ICSA_BLOCK * p.v_st, p.v_st, wave, lane);
+    } else {
+      const int ch = t - n_ex;
+      bw_dma_rows(kt, kcb + (int64_t)ch * ICSA_BLOCK * ICSA_D, ICSA_D, wave, lane);
+      bw_dma_rows(kt + K_TILE_BYTES, vcb + (int64_t)ch * ICSA_BLOCK * ICSA_D, ICSA_D, wave, lane);
+    }
+  };
+
   floatx16 dq[4] = {};
   floatx16 s[2], dp[2];
   bf16x8 dsf[4];
-
-  // ---- exact blocks ----
-  for (int t = 0; t < p.top_k; ++t) {
-    const int j = src_l[t];
-    if (j < 0) continue;
-    __syncthreads();                                   // previous tiles consumed
-    bw_row_tile(ks, kb + (int64_t)j * ICSA_BLOCK * p.k_st, p.k_st);
-    bw_row_tile(vs, vb + (int64_t)j * ICSA_BLOCK * p.v_st, p.v_st);
-    bw_t_tile(kts, ktb + (int64_t)j * ICSA_BLOCK, p.TKV);
-    __syncthreads();
-    qk_tile(s, ks, qf);
-    qk_tile(dp, vs, dof);
-#pragma unroll
-    for (int sub = 0; sub < 2; ++sub)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const float pr = __builtin_amdgcn_exp2f(fmaf(s[sub][e], p.scale_log2, -lse));
-        dsf[2 * sub + (e >> 3)][e & 7] = (bf16)(pr * (dp[sub][e] - dd));
-      }
-    pv_tile(dq, kts, dsf);
-  }
-
-  // ---- interval chunks: unselected compressed blocks, score / 64, dS / 64 ----
   const float c64 = p.scale_log2 * (1.0f / 64.0f);
-  for (int ch = 0; ch < p.nc; ++ch) {
-    __syncthreads();
-    bw_row_tile(ks, p.kcb + ((int64_t)bh * p.NKVp + ch * ICSA_BLOCK) * ICSA_D, ICSA_D);
-    bw_row_tile(vs, p.vcb + ((int64_t)bh * p.NKVp + ch * ICSA_BLOCK) * ICSA_D, ICSA_D);
-    bw_t_tile(kts, p.kct + (int64_t)bh * ICSA_D * p.NKVp + ch * ICSA_BLOCK, p.NKVp);
-    __syncthreads();
-    qk_tile(s, ks, qf);
-    qk_tile(dp, vs, dof);
-    const unsigned long long selm = sel_l[ch];
+  issue(0);                                            // T >= nc >= 1
+  for (int t = 0; t < T; ++t) {
+    const bool more = t + 1 < T;
+    if (more) {
+      issue(t + 1);                                    // the other buffer, free since step t - 1
+      BW_WAIT(16);                                     // step t's tiles
+    } else {
+      BW_WAIT(0);
+    }
+    ATT_BARRIER();
+    const unsigned char* ks = smem_q + (t & 1) * 2 * K_TILE_BYTES;
+    qk_tile(s, reinterpret_cast<const bf16*>(ks), qf);                  // S^T[key][query]
+    qk_tile(dp, reinterpret_cast<const bf16*>(ks + K_TILE_BYTES), dof); // dP^T
+    if (t < n_ex) {
 #pragma unroll
-    for (int sub = 0; sub < 2; ++sub)
+      for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int jj = 32 * sub + acc_row(e, lane);
-        const bool masked = (ch * ICSA_BLOCK + jj >= p.NKV) || ((selm >> jj) & 1ull);
-        const float pr = masked ? 0.f : __builtin_amdgcn_exp2f(fmaf(s[sub][e], c64, -lse));
-        dsf[2 * sub + (e >> 3)][e & 7] = (bf16)(pr * (dp[sub][e] - 64.0f * dd) * (1.0f / 64.0f));
-      }
-    pv_tile(dq, kts, dsf);
+        for (int e = 0; e < 16; ++e) {
+          const float pr = __builtin_amdgcn_exp2f(fmaf(s[sub][e], p.scale_log2, -lse));
+          dsf[2 * sub + (e >> 3)][e & 7] = (bf16)(pr * (dp[sub][e] - dd));
+        }
+    } else {                                           // unselected block sums: score / 64, dS / 64
+      const int ch = t - n_ex;
+      const unsigned long long selm = sel_l[ch];
+#pragma unroll
+      for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int jj = 32 * sub + acc_row(e, lane);
+          const bool masked = (ch * ICSA_BLOCK + jj >= p.NKV) || ((selm >> jj) & 1ull);
+          const float pr = masked ? 0.f : __builtin_amdgcn_exp2f(fmaf(s[sub][e], c64, -lse));
+          dsf[2 * sub + (e >> 3)][e & 7] = (bf16)(pr * (dp[sub][e] - 64.0f * dd) * (1.0f / 64.0f));
+        }
+    }
+    pv_tile_tr(dq, ks, tro, dsf);                      // dQ^T += K^T dS^T
+    ATT_BARRIER();                                     // buffer t & 1 consumed
   }
 
   // ---- epilogue: dq = scale * acc ----
   __syncthreads();
-  float* o_lds = reinterpret_cast<float*>(smem + wave * BW_STAGE_BYTES);
+  float* o_lds = reinterpret_cast<float*>(smem_q + wave * BW_STAGE_BYTES);
   stage_o(o_lds, dq, p.scale);
   __syncthreads();
   AlphaView none;
@@ -225,23 +275,23 @@ __global__ void __launch_bounds__(BW_THREADS) icsa_sparse_bwd_dq_kernel(SparseBw
 
 // ------------------------------------------------------------------------------------------
 // dk / dv: kInterval = true -> interval partials per (chunk, query range);
-//          kInterval = false -> exact part per key block + the summed partials
+//          kInterval = false -> exact part per key block + the summed partials.
+// Per visited query block: its Q and dO rows plus lse (wave 0) / D (wave 1), 17 DMA per
+// wave, land in one of two buffers while the previous block's S = Q K^T, dP = dO V^T,
+// dV^T += dO^T P and dK^T += Q^T dS run (Q^T, dO^T read transposed from the rows).
 // ------------------------------------------------------------------------------------------
-#define BWKV_TILES_BYTES (4 * K_TILE_BYTES)
-#define BWKV_LDS_BYTES (BWKV_TILES_BYTES + 2 * 64 * 4 + 2 * ICSA_D * 4 + BW_MAX_NQ * 2 + 16)
+#define BWKV_BUF_BYTES (2 * K_TILE_BYTES + 2 * 64 * 4)      // Q rows, dO rows, lse, D
+#define BWKV_LIST_BYTES 8192                 // exact: u16 query list; interval: u64 selection words
+#define BWKV_LDS_BYTES (2 * BWKV_BUF_BYTES + 2 * ICSA_D * 4 + BWKV_LIST_BYTES + 16)
 
 template <bool kInterval>
 __global__ void __launch_bounds__(BW_THREADS) icsa_sparse_bwd_dkv_kernel(SparseBwdParams p) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem_dyn[];
-  bf16* qs = reinterpret_cast<bf16*>(smem_dyn);
-  bf16* dos = reinterpret_cast<bf16*>(smem_dyn + K_TILE_BYTES);
-  bf16* qts = reinterpret_cast<bf16*>(smem_dyn + 2 * K_TILE_BYTES);
-  bf16* dots = reinterpret_cast<bf16*>(smem_dyn + 3 * K_TILE_BYTES);
-  float* lse_l = reinterpret_cast<float*>(smem_dyn + BWKV_TILES_BYTES);
-  float* dd_l = lse_l + 64;
-  float* ivec = dd_l + 64;                             // [2][128] interval sums (exact kernel)
-  unsigned short* qlist = reinterpret_cast<unsigned short*>(ivec + 2 * ICSA_D);
-  int* qcount = reinterpret_cast<int*>(qlist + BW_MAX_NQ);
+  float* ivec = reinterpret_cast<float*>(smem_dyn + 2 * BWKV_BUF_BYTES);   // [2][128] interval sums
+  unsigned char* list = reinterpret_cast<unsigned char*>(ivec + 2 * ICSA_D);
+  unsigned short* qlist = reinterpret_cast<unsigned short*>(list);
+  unsigned long long* wlist = reinterpret_cast<unsigned long long*>(list);
+  int* qcount = reinterpret_cast<int*>(list + BWKV_LIST_BYTES);
 
   const int n_work = kInterval ? p.B * p.H * p.nc * p.nsplit : p.B * p.H * p.NKV;
   const int work = xcd_remap(blockIdx.x, n_work);
@@ -270,12 +320,17 @@ __global__ void __launch_bounds__(BW_THREADS) icsa_sparse_bwd_dkv_kernel(SparseB
     load_q_frags(kf, p.k + (int64_t)b * p.k_sb + (int64_t)h * p.k_sh + (int64_t)key0 * p.k_st, p.k_st, 32);
     load_q_frags(vf, p.v + (int64_t)b * p.v_sb + (int64_t)h * p.v_sh + (int64_t)key0 * p.v_st, p.v_st, 32);
   }
+  int tro[2][4];
+  tr_offsets(tro, lane);
 
   // query blocks to visit, ascending
   int i_begin = 0, i_count;
   if (kInterval) {
     i_begin = split * p.qb_per_split;
     i_count = max(0, min(p.NQ, i_begin + p.qb_per_split) - i_begin);
+    for (int u = tid; u < i_count; u += BW_THREADS)
+      wlist[u] = p.selbits[((int64_t)bh * p.NQ + i_begin + u) * p.nc + blk];
+    __syncthreads();
   } else {
     if (wave == 0) {
       const int w = blk >> 6;
@@ -302,28 +357,39 @@ __global__ void __launch_bounds__(BW_THREADS) icsa_sparse_bwd_dkv_kernel(SparseB
 
   const bf16* qb0 = p.q + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh;
   const bf16* dob0 = p.dout + (int64_t)b * p.do_sb + (int64_t)h * p.do_sh;
-  const bf16* qtb = p.qt + (int64_t)bh * ICSA_D * p.TQ;
-  const bf16* dotb = p.dot + (int64_t)bh * ICSA_D * p.TQ;
+  const float* rowvec = (wave == 0 ? p.lse : p.dvec) + (int64_t)bh * p.TQ;
+  auto qblock = [&](int n) -> int { return kInterval ? i_begin + n : (int)qlist[n]; };
+  auto issue = [&](int n) {
+    const int i = qblock(n);
+    unsigned char* buf = smem_dyn + (n & 1) * BWKV_BUF_BYTES;
+    bw_dma_rows(buf, qb0 + (int64_t)i * ICSA_BLOCK * p.q_st, p.q_st, wave, lane);
+    bw_dma_rows(buf + K_TILE_BYTES, dob0 + (int64_t)i * ICSA_BLOCK * p.do_st, p.do_st, wave, lane);
+    const __amdgpu_buffer_rsrc_t rr = make_rsrc(rowvec + (int64_t)i * ICSA_BLOCK, ICSA_BLOCK * 4);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rr, (lds_ptr)(buf + 2 * K_TILE_BYTES + wave * 256), 4,
+                                             lane * 4, 0, 0, 0);
+  };
+
   floatx16 dk[4] = {}, dv[4] = {};
   floatx16 s[2], dp[2];
   bf16x8 pf[4], dsf[4];
-
+  if (i_count > 0) issue(0);
   for (int n = 0; n < i_count; ++n) {
-    const int i = kInterval ? i_begin + n : (int)qlist[n];
-    __syncthreads();                                   // previous tiles consumed
-    bw_row_tile(qs, qb0 + (int64_t)i * ICSA_BLOCK * p.q_st, p.q_st);
-    bw_row_tile(dos, dob0 + (int64_t)i * ICSA_BLOCK * p.do_st, p.do_st);
-    bw_t_tile(qts, qtb + (int64_t)i * ICSA_BLOCK, p.TQ);
-    bw_t_tile(dots, dotb + (int64_t)i * ICSA_BLOCK, p.TQ);
-    if (tid < 64) {
-      lse_l[tid] = p.lse[(int64_t)bh * p.TQ + i * ICSA_BLOCK + tid];
-      dd_l[tid] = p.dvec[(int64_t)bh * p.TQ + i * ICSA_BLOCK + tid];
-    }
+    const bool more = n + 1 < i_count;
     bool on = key_valid;
-    if (kInterval) on = on && ((p.selbits[((int64_t)bh * p.NQ + i) * p.nc + blk] >> (32 * wave + li)) & 1ull) == 0ull;
-    __syncthreads();
-    qk_tile(s, qs, kf);                                // S[q][key]: lane = key, elements = queries
-    qk_tile(dp, dos, vf);
+    if (kInterval) on = on && ((wlist[n] >> (32 * wave + li)) & 1ull) == 0ull;
+    if (more) {
+      issue(n + 1);                                    // the other buffer, free since block n - 1
+      BW_WAIT(17);                                     // block n's tiles
+    } else {
+      BW_WAIT(0);
+    }
+    ATT_BARRIER();
+    const unsigned char* qs = smem_dyn + (n & 1) * BWKV_BUF_BYTES;
+    const unsigned char* dos = qs + K_TILE_BYTES;
+    const float* lse_l = reinterpret_cast<const float*>(qs + 2 * K_TILE_BYTES);
+    const float* dd_l = lse_l + 64;
+    qk_tile(s, reinterpret_cast<const bf16*>(qs), kf);    // S[q][key]: lane = key, elements = queries
+    qk_tile(dp, reinterpret_cast<const bf16*>(dos), vf);  // dP[q][key]
 #pragma unroll
     for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
@@ -339,8 +405,9 @@ __global__ void __launch_bounds__(BW_THREADS) icsa_sparse_bwd_dkv_kernel(SparseB
           dsf[2 * sub + (e >> 3)][e & 7] = (bf16)(pr * (dp[sub][e] - dmul * d4[x]) * dsmul);
         }
       }
-    pv_tile(dv, dots, pf);                             // dV^T[d][key] += dO^T P
-    pv_tile(dk, qts, dsf);                             // dK^T[d][key] += Q^T dS
+    pv_tile_tr(dv, dos, tro, pf);                      // dV^T[d][key] += dO^T P
+    pv_tile_tr(dk, qs, tro, dsf);                      // dK^T[d][key] += Q^T dS
+    ATT_BARRIER();                                     // buffer n & 1 consumed
   }
 
   __syncthreads();
@@ -393,9 +460,13 @@ hipError_t launch_sparse_bwd(const SparseBwdParams& p, hipStream_t stream) {
   const int BH = p.B * p.H;
   if (BH == 0 || p.NQ == 0) return hipSuccess;
   if (p.top_k < 1 || p.top_k > BW_MAX_TOPK || p.NKV < 1 || p.nc > BW_MAX_CHUNKS ||
-      p.NKVp != p.nc * ICSA_BLOCK || p.NQ > BW_MAX_NQ || p.nsplit < 1 ||
+      p.NKVp != p.nc * ICSA_BLOCK || p.NQ > BW_MAX_NQ || p.nsplit < 1 || p.qb_per_split > 1024 ||
       (int64_t)p.nsplit * p.qb_per_split < p.NQ)
     return hipErrorInvalidValue;
+  static const hipError_t attr_q = hipFuncSetAttribute(
+      reinterpret_cast<const void*>(icsa_sparse_bwd_dq_kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+      BWQ_LDS_BYTES);
+  if (attr_q != hipSuccess) return attr_q;
   static const hipError_t attr_i = hipFuncSetAttribute(
       reinterpret_cast<const void*>(icsa_sparse_bwd_dkv_kernel<true>),
       hipFuncAttributeMaxDynamicSharedMemorySize, BWKV_LDS_BYTES);
@@ -404,7 +475,8 @@ hipError_t launch_sparse_bwd(const SparseBwdParams& p, hipStream_t stream) {
       hipFuncAttributeMaxDynamicSharedMemorySize, BWKV_LDS_BYTES);
   if (attr_i != hipSuccess) return attr_i;
   if (attr_e != hipSuccess) return attr_e;
-  hipLaunchKernelGGL(icsa_sparse_bwd_dq_kernel, dim3(xcd_grid(BH * p.NQ)), dim3(BW_THREADS), 0, stream, p);
+  hipLaunchKernelGGL(icsa_sparse_bwd_dq_kernel, dim3(xcd_grid(BH * p.NQ)), dim3(BW_THREADS), BWQ_LDS_BYTES,
+                     stream, p);
   hipLaunchKernelGGL(icsa_sparse_bwd_dkv_kernel<true>, dim3(xcd_grid(BH * p.nc * p.nsplit)), dim3(BW_THREADS),
                      BWKV_LDS_BYTES, stream, p);
   hipLaunchKernelGGL(icsa_sparse_bwd_dkv_kernel<false>, dim3(xcd_grid(BH * p.NKV)), dim3(BW_THREADS),
