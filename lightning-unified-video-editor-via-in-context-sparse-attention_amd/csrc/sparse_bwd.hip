@@ -94,12 +94,40 @@ __global__ void __launch_bounds__(256) icsa_sparse_bwd_sums_kernel(SparseBwdPara
 }
 
 // ------------------------------------------------------------------------------------------
-// Tile DMA.  A 16 KB row tile (64 rows x 128 dims, the K-tile layout of the forward) is 16
+// Tile DMA.  A 16 KB row tile (64 rows x 128 dims, swizzled by bw_swz below) is 16
 // LDS-DMA instructions, 8 per wave; each lands 1 KB at consecutive LDS addresses (lane l
 // at +16 l), so the XOR swizzle is applied on the global side.  Loads complete in issue
 // order: with the next step's tiles in flight a kernel waits with vmcnt(their count).
 // ------------------------------------------------------------------------------------------
 #define BW_WAIT(n) asm volatile("s_waitcnt vmcnt(" #n ")" ::: "memory")
+
+// Row-tile swizzle of the backward: 16-byte chunk c of row r sits at slot c ^ bw_swz(r).
+// bw_swz is a bijection of r % 16, so the 16-byte operand reads of 16 consecutive rows
+// (one chunk) hit 16 distinct slots; and it moves rows 4 a + x (x = 0..3) to different slot
+// quadrants, so a transposing read (4 rows x 4 chunk positions x 2 halves per half-wave)
+// touches 32 distinct 8-byte bank pairs.  The forward's swizzle (c ^ (r % 16)) folds those
+// 16 (row, chunk) pairs onto 4 slots.
+__device__ __forceinline__ int bw_swz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
+__device__ __forceinline__ int bw_row_off(int row, int chunk) {    // in bf16 elements
+  return row * ICSA_D + ((chunk ^ bw_swz(row)) << 3);
+}
+
+// S^T (or S) for the 64 rows of a backward row tile: s[sub] covers rows 32 sub .. 32 sub + 31.
+__device__ __forceinline__ void qk_tile_bw(floatx16 s[2], const bf16* tile, const bf16x8 bf[8]) {
+  const int lane = threadIdx.x & 63;
+  const int li = lane & 31, hl = lane >> 5;
+#pragma unroll
+  for (int sub = 0; sub < 2; ++sub) {
+    floatx16 acc = {};
+    const int row = 32 * sub + li;
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) {
+      const bf16x8 a = *reinterpret_cast<const bf16x8*>(tile + bw_row_off(row, 2 * kk + hl));
+      acc = mfma32x32x16(a, bf[kk], acc);
+    }
+    s[sub] = acc;
+  }
+}
 
 __device__ __forceinline__ void bw_dma_rows(unsigned char* tile, const bf16* base, int64_t rs, int wave,
                                             int lane) {
@@ -108,7 +136,7 @@ __device__ __forceinline__ void bw_dma_rows(unsigned char* tile, const bf16* bas
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int r = 32 * wave + 4 * i + (lane >> 4);
-    const int off = (int)(r * rs * 2) + (((lane & 15) ^ (r & 15)) << 4);
+    const int off = (int)(r * rs * 2) + (((lane & 15) ^ bw_swz(r)) << 4);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_ptr)(dst + 1024 * i), 16, off, 0, 0, 0);
   }
 }
@@ -121,7 +149,7 @@ __device__ __forceinline__ void bw_dma_rows(unsigned char* tile, const bf16* bas
 // A[d = 32 ds + l % 32][k = 8 (l / 32) + e]) with the row order of the score accumulators
 // (k -> row 16 m + 8 (e / 4) + 4 (l / 32) + e % 4), lane 16 g + s reads the 4 dims
 // 32 ds + 16 (g % 2) + 4 (s % 4) .. + 3 of row 16 m + 4 (g / 2) + s / 4 (+ 8 for e >= 4).
-// tro[h][ds]: those byte offsets in the K-tile layout for m = 0; step m adds 16 rows.
+// tro[h][ds]: those byte offsets in the row-tile layout for m = 0; step m adds 16 rows.
 // ------------------------------------------------------------------------------------------
 typedef short bw_v4s __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) bw_v4s* bw_lds_v4s;
@@ -134,7 +162,7 @@ __device__ __forceinline__ void tr_offsets(int tro[2][4], int lane) {
     for (int ds = 0; ds < 4; ++ds) {
       const int row = 4 * (g >> 1) + (s >> 2) + 8 * h;
       const int col = 32 * ds + 16 * (g & 1) + 4 * (s & 3);
-      tro[h][ds] = row * (ICSA_D * 2) + ((((col >> 3) ^ (row & 15))) << 4) + (col & 7) * 2;
+      tro[h][ds] = row * (ICSA_D * 2) + (((col >> 3) ^ bw_swz(row)) << 4) + (col & 7) * 2;
     }
 }
 
@@ -236,8 +264,8 @@ __global__ void __launch_bounds__(BW_THREADS) icsa_sparse_bwd_dq_kernel(SparseBw
     }
     ATT_BARRIER();
     const unsigned char* ks = smem_q + (t & 1) * 2 * K_TILE_BYTES;
-    qk_tile(s, reinterpret_cast<const bf16*>(ks), qf);                  // S^T[key][query]
-    qk_tile(dp, reinterpret_cast<const bf16*>(ks + K_TILE_BYTES), dof); // dP^T
+    qk_tile_bw(s, reinterpret_cast<const bf16*>(ks), qf);                  // S^T[key][query]
+    qk_tile_bw(dp, reinterpret_cast<const bf16*>(ks + K_TILE_BYTES), dof); // dP^T
     if (t < n_ex) {
 #pragma unroll
       for (int sub = 0; sub < 2; ++sub)
@@ -388,8 +416,8 @@ __global__ void __launch_bounds__(BW_THREADS) icsa_sparse_bwd_dkv_kernel(SparseB
     const unsigned char* dos = qs + K_TILE_BYTES;
     const float* lse_l = reinterpret_cast<const float*>(qs + 2 * K_TILE_BYTES);
     const float* dd_l = lse_l + 64;
-    qk_tile(s, reinterpret_cast<const bf16*>(qs), kf);    // S[q][key]: lane = key, elements = queries
-    qk_tile(dp, reinterpret_cast<const bf16*>(dos), vf);  // dP[q][key]
+    qk_tile_bw(s, reinterpret_cast<const bf16*>(qs), kf);    // S[q][key]: lane = key, elements = queries
+    qk_tile_bw(dp, reinterpret_cast<const bf16*>(dos), vf);  // dP[q][key]
 #pragma unroll
     for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
