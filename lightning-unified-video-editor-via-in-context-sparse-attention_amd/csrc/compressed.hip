@@ -22,54 +22,101 @@ __device__ __forceinline__ float block_size_f(int blk, int NB, int S) {
 }
 
 // ---------------------------------------------------------------------------------------
-// (a) logits L = (Qs/size) (Ks/size)^T / sqrt(D), one 64x64 tile per workgroup (fp32 MFMA)
+// (a) logits L = (Qs/size) (Ks/size)^T / sqrt(D) with fp32 MFMA (32x32x2).  Workgroup =
+//     4 waves = 128 query rows (wave w: rows 32 w .. 32 w + 31) against one of LG_SPLIT
+//     column ranges.  A wave's A operands stay in registers for the whole range (lane
+//     (li, hl) holds row li's dims 64 hl .. 64 hl + 63); 32-column K tiles pass through a
+//     double-buffered LDS ring, the next tile prefetched into registers while the current
+//     one is multiplied.  MFMA step kk contracts dims kk and 64 + kk, kk ascending: a fixed
+//     order, so repeated runs are bitwise identical.
 // ---------------------------------------------------------------------------------------
+#define LG_SPLIT 4
+#define LG_ROWS 128
+#define LG_COLS 32
+
 __global__ void __launch_bounds__(256) icsa_compressed_logits_kernel(CompressedParams p) {
-  __shared__ float qs[64][132];
-  __shared__ float ks[64][132];
-  const int ct = blockIdx.x, rt = blockIdx.y, bh = blockIdx.z;
+  __shared__ float ks[2][LG_COLS][132];
+  const int rt = blockIdx.x, cs = blockIdx.y, bh = blockIdx.z;
   const int NB = p.NB;
+  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63;
+  const int li = l & 31, hl = l >> 5;
   const float* qbase = p.qsum + (int64_t)bh * NB * ICSA_D;
   const float* kbase = p.ksum + (int64_t)bh * NB * ICSA_D;
-  for (int e = threadIdx.x; e < 64 * 32; e += 256) {
-    const int r = e >> 5, c4 = e & 31;
-    floatx4 qv = {0.f, 0.f, 0.f, 0.f}, kv = {0.f, 0.f, 0.f, 0.f};
-    const int qrow = rt * 64 + r, krow = ct * 64 + r;
-    if (qrow < NB) {
-      qv = *reinterpret_cast<const floatx4*>(qbase + (int64_t)qrow * ICSA_D + 4 * c4);
-      const float sz = block_size_f(qrow, NB, p.S);
+
+  // A operands: this lane's query row, dims 64 hl .. 64 hl + 63, divided by the block size
+  float a[64];
+  {
+    const int row = rt * LG_ROWS + 32 * w + li;
+    if (row < NB) {
+      const float sz = block_size_f(row, NB, p.S);
+      const float* src = qbase + (int64_t)row * ICSA_D + 64 * hl;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) qv[i] = qv[i] / sz;
+      for (int c4 = 0; c4 < 16; ++c4) {
+        const floatx4 v = *reinterpret_cast<const floatx4*>(src + 4 * c4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) a[4 * c4 + e] = v[e] / sz;
+      }
+    } else {
+#pragma unroll
+      for (int kk = 0; kk < 64; ++kk) a[kk] = 0.f;
     }
-    if (krow < NB) {
-      kv = *reinterpret_cast<const floatx4*>(kbase + (int64_t)krow * ICSA_D + 4 * c4);
-      const float sz = block_size_f(krow, NB, p.S);
+  }
+
+  const int n_ct = (NB + LG_COLS - 1) / LG_COLS;
+  const int per = (n_ct + LG_SPLIT - 1) / LG_SPLIT;
+  const int t0 = cs * per, t1 = min(n_ct, t0 + per);
+  if (t0 >= t1) return;                                // uniform for the workgroup
+
+  // K tile staging: thread -> (column tid / 8, 16 dims from 16 (tid % 8))
+  const int kc = tid >> 3, kd = 16 * (tid & 7);
+  floatx4 pre[4];
+  auto load_tile = [&](int t) {
+    const int col = t * LG_COLS + kc;
+    if (col < NB) {
+      const float sz = block_size_f(col, NB, p.S);
+      const float* src = kbase + (int64_t)col * ICSA_D + kd;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) kv[i] = kv[i] / sz;
+      for (int q = 0; q < 4; ++q) {
+        pre[q] = *reinterpret_cast<const floatx4*>(src + 4 * q);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) pre[q][e] = pre[q][e] / sz;
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) pre[q] = floatx4{0.f, 0.f, 0.f, 0.f};
     }
-    *reinterpret_cast<floatx4*>(&qs[r][4 * c4]) = qv;
-    *reinterpret_cast<floatx4*>(&ks[r][4 * c4]) = kv;
-  }
-  __syncthreads();
-  const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
-  const int li = l & 31, hl = l >> 5;
-  const int r0 = 32 * (w & 1), c0 = 32 * (w >> 1);
-  floatx16 acc = {};
-  // lane half hl contracts d in [64*hl, 64*hl + 64); A and B use the same split.
-#pragma unroll 4
-  for (int kk = 0; kk < 64; kk += 4) {
-    const floatx4 a = *reinterpret_cast<const floatx4*>(&qs[r0 + li][64 * hl + kk]);
-    const floatx4 b = *reinterpret_cast<const floatx4*>(&ks[c0 + li][64 * hl + kk]);
+  };
+  auto store_tile = [&](int buf) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc = mfma32x32x2f32(a[j], b[j], acc);
-  }
+    for (int q = 0; q < 4; ++q) *reinterpret_cast<floatx4*>(&ks[buf][kc][kd + 4 * q]) = pre[q];
+  };
+
   const float sq = sqrtf((float)ICSA_D);
   float* out = p.P + (int64_t)bh * NB * NB;
-  const int col = ct * 64 + c0 + li;
+  load_tile(t0);
+  store_tile(0);
+  __syncthreads();
+  for (int t = t0; t < t1; ++t) {
+    const int buf = (t - t0) & 1;
+    const bool more = t + 1 < t1;
+    if (more) load_tile(t + 1);
+    floatx16 acc = {};
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int row = rt * 64 + r0 + acc_row(i, l);
-    if (row < NB && col < NB) out[(int64_t)row * NB + col] = acc[i] / sq;
+    for (int kk = 0; kk < 64; kk += 4) {
+      const floatx4 b = *reinterpret_cast<const floatx4*>(&ks[buf][li][64 * hl + kk]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc = mfma32x32x2f32(a[kk + j], b[j], acc);
+    }
+    const int col = t * LG_COLS + li;
+    if (col < NB) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int row = rt * LG_ROWS + 32 * w + acc_row(i, l);
+        if (row < NB) out[(int64_t)row * NB + col] = acc[i] / sq;
+      }
+    }
+    if (more) store_tile(buf ^ 1);                     // that buffer was read in step t - 1
+    __syncthreads();
   }
 }
 
@@ -221,7 +268,8 @@ __global__ void __launch_bounds__(512) icsa_compressed_rows_kernel(CompressedPar
 hipError_t launch_compressed(const CompressedParams& p, hipStream_t stream) {
   if (p.NB > ICSA_MAX_NB) return hipErrorInvalidValue;
   const int nt = (p.NB + 63) / 64;
-  hipLaunchKernelGGL(icsa_compressed_logits_kernel, dim3(nt, nt, p.BH), dim3(256), 0, stream, p);
+  hipLaunchKernelGGL(icsa_compressed_logits_kernel, dim3((p.NB + LG_ROWS - 1) / LG_ROWS, LG_SPLIT, p.BH),
+                     dim3(256), 0, stream, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int64_t rows = (int64_t)p.BH * p.NB;
