@@ -215,32 +215,55 @@ __global__ void __launch_bounds__(512) icsa_compressed_rows_kernel(CompressedPar
   const int n_ts = (n_t + ICSA_BLOCK - 1) / ICSA_BLOCK;
   const int tgt_rows = min(64, n_t - r_base);          // > 0 only for target strips
   floatx16 acc = {};
+  // the next chunk's logits (8 per thread: row e / 64, column e % 64 for e = tid + 512 x)
+  // and its V block sums (4 float4 per thread: block kk = e / 32, dims 4 (e % 32)) are
+  // loaded into registers while the current chunk is multiplied
+  float lg[8];
+  floatx4 vv[4];
+  auto load_chunk = [&](int k0) {
+#pragma unroll
+    for (int x = 0; x < 8; ++x) {
+      const int e = tid + 512 * x;
+      const int row = r_base + (e >> 6), col = k0 + (e & 63);
+      lg[x] = (row < NB && col < NB) ? Pbh[(int64_t)row * NB + col] : 0.f;
+    }
+#pragma unroll
+    for (int x = 0; x < 4; ++x) {
+      const int e = tid + 512 * x;
+      const int kc = k0 + (e >> 5);
+      vv[x] = kc < NB ? *reinterpret_cast<const floatx4*>(V + (int64_t)kc * ICSA_D + 4 * (e & 31))
+                      : floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+  };
   __syncthreads();
+  load_chunk(0);
   for (int k0 = 0; k0 < NB; k0 += 64) {
-    for (int e = tid; e < 64 * 64; e += 512) {
+#pragma unroll
+    for (int x = 0; x < 8; ++x) {                     // P = exp(L - m) / z, in place and to LDS
+      const int e = tid + 512 * x;
       const int r = e >> 6, kk = e & 63;
       const int row = r_base + r, col = k0 + kk;
       float pv = 0.f;
       if (row < NB && col < NB) {
-        float* Lp = Pbh + (int64_t)row * NB + col;
-        pv = expf(*Lp - row_m[r]) * row_iz[r];
-        *Lp = pv;
+        pv = expf(lg[x] - row_m[r]) * row_iz[r];
+        Pbh[(int64_t)row * NB + col] = pv;
       }
       ps[r][kk] = pv;
     }
-    for (int e = tid; e < 64 * 32; e += 512) {
-      const int kk = e >> 5, c4 = e & 31;
-      const int kc = k0 + kk;
-      floatx4 vv = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int x = 0; x < 4; ++x) {                     // V block means
+      const int e = tid + 512 * x;
+      const int kk = e >> 5, kc = k0 + kk;
+      floatx4 v = vv[x];
       if (kc < NB) {
-        vv = *reinterpret_cast<const floatx4*>(V + (int64_t)kc * ICSA_D + 4 * c4);
         const float inv = 1.f / block_size_f(kc, NB, p.S);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) vv[i] *= inv;
+        for (int q = 0; q < 4; ++q) v[q] *= inv;
       }
-      *reinterpret_cast<floatx4*>(&vs[kk][4 * c4]) = vv;
+      *reinterpret_cast<floatx4*>(&vs[kk][4 * (e & 31)]) = v;
     }
     __syncthreads();
+    if (k0 + 64 < NB) load_chunk(k0 + 64);
 #pragma unroll 2
     for (int s = 0; s < 32; s += 4) {
       const floatx4 a = *reinterpret_cast<const floatx4*>(&ps[r0 + li][32 * hl + s]);
