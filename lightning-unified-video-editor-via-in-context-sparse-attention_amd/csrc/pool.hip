@@ -3,7 +3,7 @@
 // Reference: editing_sparse_attention.py:89-111 (pad + block mean, compress_seq :37-55) and
 // the block-sum kernels tilelang_kernels.py:33-120 / triton_kernels.py:16-119.
 //
-// One workgroup per (64-token block, b*h).  Each of the three inputs is read exactly once:
+// One workgroup per (b*h, 64-token block), heads fastest.  Each input is read exactly once:
 //   * fp32 block sums        -> sums[i]  [B, H, NB, D]   (means = sums / block size)
 //   * optional bf16 copy     -> xb[i]    same strides as a contiguous [B, S, H, D]
 //   * optional V transposed  -> vt       [B, H, D, Sp] bf16, kv_slot() order, zero padded
@@ -11,13 +11,53 @@
 // and the transposed copy is zero for padding tokens.
 #include "icsa_kernels.h"
 
+// Raw storage of 8 consecutive elements of one row (one thread's share of a 64-token row).
+template <typename T> struct Raw8;
+template <> struct Raw8<bf16> {
+  bf16x8 v;
+  __device__ __forceinline__ void load(const bf16* p) { v = *reinterpret_cast<const bf16x8*>(p); }
+  __device__ __forceinline__ void zero() {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = (bf16)0.f;
+  }
+  __device__ __forceinline__ void to_f32(float o[8]) const {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = (float)v[e];
+  }
+};
+template <> struct Raw8<float> {
+  floatx4 a, b;
+  __device__ __forceinline__ void load(const float* p) {
+    a = *reinterpret_cast<const floatx4*>(p);
+    b = *reinterpret_cast<const floatx4*>(p + 4);
+  }
+  __device__ __forceinline__ void zero() { a = floatx4{0.f, 0.f, 0.f, 0.f}; b = a; }
+  __device__ __forceinline__ void to_f32(float o[8]) const {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) { o[e] = a[e]; o[4 + e] = b[e]; }
+  }
+};
+
+// Thread t covers chunk c = t % 16 (8 of the 128 dims) of rows g + 16 j, g = t / 16.
 template <typename T>
-__device__ __forceinline__ void pool_one(const PoolParams& p, int i, int n, int b, int h,
+__device__ __forceinline__ void pool_load(const PoolParams& p, int i, int n, int b, int h, Raw8<T> (&r)[4]) {
+  const int t = threadIdx.x;
+  const int c = t & 15, g = t >> 4;
+  const T* base = reinterpret_cast<const T*>(p.x[i].p) + (int64_t)b * p.x[i].sb + (int64_t)h * p.x[i].sh;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int tok = n * ICSA_BLOCK + g + 16 * j;
+    if (tok < p.S) r[j].load(base + (int64_t)tok * p.x[i].ss + 8 * c);
+    else r[j].zero();
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ void pool_one(const PoolParams& p, int i, int n, int b, int h, const Raw8<T> (&rows)[4],
                                          float (*red)[ICSA_D + 4], bf16 (*vtile)[ICSA_D + 8]) {
   const int t = threadIdx.x;
   const int c = t & 15;          // 16 chunks of 8 elements across D = 128
   const int g = t >> 4;          // 16 row groups, 4 rows each
-  const T* base = reinterpret_cast<const T*>(p.x[i].p) + (int64_t)b * p.x[i].sb + (int64_t)h * p.x[i].sh;
   float acc[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) acc[e] = 0.f;
@@ -28,12 +68,7 @@ __device__ __forceinline__ void pool_one(const PoolParams& p, int i, int n, int 
     const int r = g + 16 * j;
     const int tok = n * ICSA_BLOCK + r;
     float v[8];
-    if (tok < p.S) {
-      load8_f32<T>(base + (int64_t)tok * p.x[i].ss + 8 * c, v);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] = 0.f;
-    }
+    rows[j].to_f32(v);           // rows past S were loaded as zeros
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[e] += v[e];
     if (want_copy && tok < p.S) {
@@ -79,17 +114,24 @@ template <typename T0, typename T1, typename T2>
 __global__ void __launch_bounds__(256) icsa_pool_kernel(PoolParams p) {
   __shared__ float red[16][ICSA_D + 4];
   __shared__ bf16 vtile[ICSA_BLOCK][ICSA_D + 8];
-  const int n = blockIdx.x;
-  const int bh = blockIdx.y;
+  const int bh = blockIdx.x;          // heads fastest: neighbouring workgroups read adjacent
+  const int n = blockIdx.y;           // 256-byte head rows of the same tokens
   const int b = bh / p.H, h = bh % p.H;
-  if (p.x[0].p) pool_one<T0>(p, 0, n, b, h, red, vtile);
-  if (p.x[1].p) pool_one<T1>(p, 1, n, b, h, red, vtile);
-  if (p.x[2].p) pool_one<T2>(p, 2, n, b, h, red, vtile);
+  // every present input's rows are requested before any is reduced
+  Raw8<T0> r0[4];
+  Raw8<T1> r1[4];
+  Raw8<T2> r2[4];
+  if (p.x[0].p) pool_load<T0>(p, 0, n, b, h, r0);
+  if (p.x[1].p) pool_load<T1>(p, 1, n, b, h, r1);
+  if (p.x[2].p) pool_load<T2>(p, 2, n, b, h, r2);
+  if (p.x[0].p) pool_one<T0>(p, 0, n, b, h, r0, red, vtile);
+  if (p.x[1].p) pool_one<T1>(p, 1, n, b, h, r1, red, vtile);
+  if (p.x[2].p) pool_one<T2>(p, 2, n, b, h, r2, red, vtile);
 }
 
 // Host launcher: dtypes select the instantiation (bf16 / fp32 per input).
 hipError_t launch_pool(const PoolParams& p, hipStream_t stream) {
-  dim3 grid(p.NB, p.B * p.H);
+  dim3 grid(p.B * p.H, p.NB);
   dim3 block(256);
   const int d0 = p.x[0].p ? p.x[0].dtype : ICSA_DT_BF16;
   const int d1 = p.x[1].p ? p.x[1].dtype : ICSA_DT_BF16;
