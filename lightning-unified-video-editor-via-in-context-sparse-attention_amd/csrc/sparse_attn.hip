@@ -42,7 +42,7 @@
 #define SP_STAGE_BYTES (32 * O_LDS_STRIDE * 4)
 #define SP_BUF_BYTES (SP_STAGE_BYTES > K_TILE_BYTES ? SP_STAGE_BYTES : K_TILE_BYTES)
 #define SP_RESCALE_LOG2 8.0f
-#define SP_PF 3                          // MFMA operand read-ahead (steps)
+#define SP_PF 2                          // MFMA operand read-ahead (steps); 3 spills at 256 VGPRs
 #define SP_DMA_PER_TILE 8                // LDS-DMA instructions per wave per K or V^T tile
 
 // vmcnt waits: "all but the newest tile" / "everything".  Loads complete in issue order.
