@@ -16,7 +16,22 @@
 // conflicts: K tile row r chunk c at c ^ (r & 15); V^T tile row d chunk c at c ^ ((d>>1)&7).
 #pragma once
 
+#include <atomic>
+
 #include "icsa_common.h"
+
+// Raises a kernel's dynamic-LDS limit to `bytes` on the current device, once per device
+// (the attribute belongs to the device's copy of the kernel).  `done`: one bit per device.
+inline hipError_t ensure_lds_limit(const void* func, int bytes, std::atomic<unsigned>* done) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  const unsigned bit = dev >= 0 && dev < 32 ? (1u << dev) : 0u;
+  if (bit != 0u && (done->load(std::memory_order_acquire) & bit)) return hipSuccess;
+  e = hipFuncSetAttribute(func, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  if (e == hipSuccess && bit != 0u) done->fetch_or(bit, std::memory_order_release);
+  return e;
+}
 
 #define ATT_BN 64                         // keys per tile
 #define K_TILE_BYTES (ATT_BN * ICSA_D * 2)    // 16 KB

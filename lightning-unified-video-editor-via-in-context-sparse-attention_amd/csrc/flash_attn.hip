@@ -286,9 +286,8 @@ hipError_t launch_flash(const FlashParams& p, hipStream_t stream) {
   // per-(b, h) slices must be addressable with 32-bit buffer offsets
   if ((int64_t)p.Sk * p.k_ss * 2 > 0x7fffffffLL || (int64_t)ICSA_D * p.vt_sd * 2 > 0x7fffffffLL)
     return hipErrorInvalidValue;
-  static const hipError_t attr = hipFuncSetAttribute(
-      reinterpret_cast<const void*>(icsa_flash_kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-      FA_LDS_BYTES);
+  static std::atomic<unsigned> lds_set{0u};
+  const hipError_t attr = ensure_lds_limit(reinterpret_cast<const void*>(icsa_flash_kernel), FA_LDS_BYTES, &lds_set);
   if (attr != hipSuccess) return attr;
   hipLaunchKernelGGL(icsa_flash_kernel, dim3(xcd_grid(n_work)), dim3(FA_THREADS), FA_LDS_BYTES, stream, p);
   return hipGetLastError();

@@ -491,18 +491,13 @@ hipError_t launch_sparse_bwd(const SparseBwdParams& p, hipStream_t stream) {
       p.NKVp != p.nc * ICSA_BLOCK || p.NQ > BW_MAX_NQ || p.nsplit < 1 || p.qb_per_split > 1024 ||
       (int64_t)p.nsplit * p.qb_per_split < p.NQ)
     return hipErrorInvalidValue;
-  static const hipError_t attr_q = hipFuncSetAttribute(
-      reinterpret_cast<const void*>(icsa_sparse_bwd_dq_kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-      BWQ_LDS_BYTES);
-  if (attr_q != hipSuccess) return attr_q;
-  static const hipError_t attr_i = hipFuncSetAttribute(
-      reinterpret_cast<const void*>(icsa_sparse_bwd_dkv_kernel<true>),
-      hipFuncAttributeMaxDynamicSharedMemorySize, BWKV_LDS_BYTES);
-  static const hipError_t attr_e = hipFuncSetAttribute(
-      reinterpret_cast<const void*>(icsa_sparse_bwd_dkv_kernel<false>),
-      hipFuncAttributeMaxDynamicSharedMemorySize, BWKV_LDS_BYTES);
-  if (attr_i != hipSuccess) return attr_i;
-  if (attr_e != hipSuccess) return attr_e;
+  static std::atomic<unsigned> set_q{0u}, set_i{0u}, set_e{0u};
+  hipError_t attr = ensure_lds_limit(reinterpret_cast<const void*>(icsa_sparse_bwd_dq_kernel), BWQ_LDS_BYTES, &set_q);
+  if (attr != hipSuccess) return attr;
+  attr = ensure_lds_limit(reinterpret_cast<const void*>(icsa_sparse_bwd_dkv_kernel<true>), BWKV_LDS_BYTES, &set_i);
+  if (attr != hipSuccess) return attr;
+  attr = ensure_lds_limit(reinterpret_cast<const void*>(icsa_sparse_bwd_dkv_kernel<false>), BWKV_LDS_BYTES, &set_e);
+  if (attr != hipSuccess) return attr;
   hipLaunchKernelGGL(icsa_sparse_bwd_dq_kernel, dim3(xcd_grid(BH * p.NQ)), dim3(BW_THREADS), BWQ_LDS_BYTES,
                      stream, p);
   hipLaunchKernelGGL(icsa_sparse_bwd_dkv_kernel<true>, dim3(xcd_grid(BH * p.nc * p.nsplit)), dim3(BW_THREADS),

@@ -183,6 +183,8 @@ def sparse_piecewise_attn_1st_intervals_bwd_hip(do, q, k, v, out, lse, indices, 
     NQ = TQ // BLOCK_M
     _require(do.shape == q.shape and out.shape == q.shape, "do / out must be [B, H, TQ, D] like q")
     _require(do.dtype == torch.bfloat16 and out.dtype == torch.bfloat16, "do / out must be bfloat16")
+    _require(all(t.device == q.device for t in (k, v, do, out, lse, indices)),
+             "q, k, v, do, out, lse and indices must be on the same GPU")
     _require(tuple(lse.shape) == (B, H, TQ) and lse.dtype == torch.float32, "lse must be f32 [B, H, TQ]")
     _require(indices.dim() == 4 and tuple(indices.shape[:3]) == (B, H, NQ),
              f"indices must be [B, H, {NQ}, top_k]")
