@@ -112,21 +112,31 @@ __device__ __forceinline__ int bw_row_off(int row, int chunk) {    // in bf16 el
   return row * ICSA_D + ((chunk ^ bw_swz(row)) << 3);
 }
 
+#define BW_PF 3                 // MFMA operand read-ahead (steps)
+
 // S^T (or S) for the 64 rows of a backward row tile: s[sub] covers rows 32 sub .. 32 sub + 31.
+// Step t uses sub = t % 2 and dims 16 (t / 2) .. + 15; operands are read BW_PF steps ahead
+// (with one wave per SIMD nothing else hides the LDS latency).
 __device__ __forceinline__ void qk_tile_bw(floatx16 s[2], const bf16* tile, const bf16x8 bf[8]) {
   const int lane = threadIdx.x & 63;
   const int li = lane & 31, hl = lane >> 5;
+  auto ld = [&](int t) -> bf16x8 {
+    return *reinterpret_cast<const bf16x8*>(tile + bw_row_off(32 * (t & 1) + li, 2 * (t >> 1) + hl));
+  };
+  bf16x8 a[16];
 #pragma unroll
-  for (int sub = 0; sub < 2; ++sub) {
-    floatx16 acc = {};
-    const int row = 32 * sub + li;
+  for (int t = 0; t < BW_PF; ++t) a[t] = ld(t);
+  __builtin_amdgcn_sched_barrier(0);
+  floatx16 acc0 = {}, acc1 = {};
 #pragma unroll
-    for (int kk = 0; kk < 8; ++kk) {
-      const bf16x8 a = *reinterpret_cast<const bf16x8*>(tile + bw_row_off(row, 2 * kk + hl));
-      acc = mfma32x32x16(a, bf[kk], acc);
-    }
-    s[sub] = acc;
+  for (int t = 0; t < 16; ++t) {
+    if (t + BW_PF < 16) a[t + BW_PF] = ld(t + BW_PF);
+    if (t & 1) acc1 = mfma32x32x16(a[t], bf[t >> 1], acc1);
+    else acc0 = mfma32x32x16(a[t], bf[t >> 1], acc0);
+    __builtin_amdgcn_sched_barrier(0);
   }
+  s[0] = acc0;
+  s[1] = acc1;
 }
 
 __device__ __forceinline__ void bw_dma_rows(unsigned char* tile, const bf16* base, int64_t rs, int wave,
@@ -167,18 +177,26 @@ __device__ __forceinline__ void tr_offsets(int tro[2][4], int lane) {
 }
 
 // o[4 d-subtiles] += X^T P for a row tile X (bytes at `tile`); p[m]: bf16 B operand of
-// 16-row step m, straight from the score accumulators.
+// 16-row step m, straight from the score accumulators.  Step t = 4 m + ds; each operand is
+// two transposing reads, issued BW_PF steps ahead.
 __device__ __forceinline__ void pv_tile_tr(floatx16 o[4], const unsigned char* tile, const int tro[2][4],
                                            const bf16x8 p[4]) {
+  auto ld = [&](int t) -> bf16x8 {
+    const int m = t >> 2, ds = t & 3;
+    const bw_v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((bw_lds_v4s)(tile + tro[0][ds] + m * 16 * ICSA_D * 2));
+    const bw_v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((bw_lds_v4s)(tile + tro[1][ds] + m * 16 * ICSA_D * 2));
+    const short __attribute__((ext_vector_type(8))) a8 = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    return __builtin_bit_cast(bf16x8, a8);
+  };
+  bf16x8 a[16];
 #pragma unroll
-  for (int m = 0; m < 4; ++m) {
+  for (int t = 0; t < BW_PF; ++t) a[t] = ld(t);
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int ds = 0; ds < 4; ++ds) {
-      const bw_v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((bw_lds_v4s)(tile + tro[0][ds] + m * 16 * ICSA_D * 2));
-      const bw_v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((bw_lds_v4s)(tile + tro[1][ds] + m * 16 * ICSA_D * 2));
-      const short __attribute__((ext_vector_type(8))) a8 = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-      o[ds] = mfma32x32x16(__builtin_bit_cast(bf16x8, a8), p[m], o[ds]);
-    }
+  for (int t = 0; t < 16; ++t) {
+    if (t + BW_PF < 16) a[t + BW_PF] = ld(t + BW_PF);
+    o[t & 3] = mfma32x32x16(a[t], p[t >> 2], o[t & 3]);
+    __builtin_amdgcn_sched_barrier(0);
   }
 }
 
