@@ -434,25 +434,65 @@ __global__ void __launch_bounds__(BW_THREADS) icsa_sparse_bwd_dkv_kernel(SparseB
     const unsigned char* dos = qs + K_TILE_BYTES;
     const float* lse_l = reinterpret_cast<const float*>(qs + 2 * K_TILE_BYTES);
     const float* dd_l = lse_l + 64;
-    qk_tile_bw(s, reinterpret_cast<const bf16*>(qs), kf);    // S[q][key]: lane = key, elements = queries
-    qk_tile_bw(dp, reinterpret_cast<const bf16*>(dos), vf);  // dP[q][key]
-#pragma unroll
-    for (int sub = 0; sub < 2; ++sub)
+    // One stream of 64 MFMAs, operands read BW_PF steps ahead, with the elementwise work
+    // slotted between MFMAs that do not depend on it (one wave per SIMD: nothing else
+    // fills the matrix pipe while this wave runs VALU code):
+    //   t  0..15  S and dP of query rows 0-31   (t even: S = Q K^T, odd: dP = dO V^T; kk = t / 2 % 8)
+    //   t 16..31  S and dP of rows 32-63        + P, dS of rows 0-31 (one element per MFMA)
+    //   t 32..63  u = t - 32: m = u / 8, ds = u / 2 % 4; u even: dV^T += dO^T P, odd:
+    //             dK^T += Q^T dS                + P, dS of rows 32-63 during u < 16
+    const bf16* qsb = reinterpret_cast<const bf16*>(qs);
+    const bf16* dosb = reinterpret_cast<const bf16*>(dos);
+    const int hl = lane >> 5;
+    auto ld = [&](int t) -> bf16x8 {
+      if (t < 32) {
+        const int sub = t >> 4, kk = (t & 15) >> 1;
+        return *reinterpret_cast<const bf16x8*>(((t & 1) ? dosb : qsb) + bw_row_off(32 * sub + li, 2 * kk + hl));
+      }
+      const int u = t - 32, m = u >> 3, ds = (u >> 1) & 3;
+      const unsigned char* tile = (u & 1) ? qs : dos;
+      const bw_v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((bw_lds_v4s)(tile + tro[0][ds] + m * 16 * ICSA_D * 2));
+      const bw_v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((bw_lds_v4s)(tile + tro[1][ds] + m * 16 * ICSA_D * 2));
+      const short __attribute__((ext_vector_type(8))) a8 = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      return __builtin_bit_cast(bf16x8, a8);
+    };
+    floatx4 l4[2][4], d4[2][4];                        // lse / D of the rows each lane holds
+    auto ld_rows = [&](int sub) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const int r0 = 32 * sub + 8 * g + 4 * (lane >> 5);    // acc_row(4 g + x, lane) = r0 + x
-        const floatx4 l4 = *reinterpret_cast<const floatx4*>(lse_l + r0);
-        const floatx4 d4 = *reinterpret_cast<const floatx4*>(dd_l + r0);
-#pragma unroll
-        for (int x = 0; x < 4; ++x) {
-          const int e = 4 * g + x;
-          const float pr = on ? __builtin_amdgcn_exp2f(fmaf(s[sub][e], cexp, -l4[x])) : 0.f;
-          pf[2 * sub + (e >> 3)][e & 7] = (bf16)pr;
-          dsf[2 * sub + (e >> 3)][e & 7] = (bf16)(pr * (dp[sub][e] - dmul * d4[x]) * dsmul);
-        }
+        const int r0 = 32 * sub + 8 * g + 4 * (lane >> 5);  // acc_row(4 g + x, lane) = r0 + x
+        l4[sub][g] = *reinterpret_cast<const floatx4*>(lse_l + r0);
+        d4[sub][g] = *reinterpret_cast<const floatx4*>(dd_l + r0);
       }
-    pv_tile_tr(dv, dos, tro, pf);                      // dV^T[d][key] += dO^T P
-    pv_tile_tr(dk, qs, tro, dsf);                      // dK^T[d][key] += Q^T dS
+    };
+    auto elem = [&](int sub, int e) {
+      const float pr = on ? __builtin_amdgcn_exp2f(fmaf(s[sub][e], cexp, -l4[sub][e >> 2][e & 3])) : 0.f;
+      pf[2 * sub + (e >> 3)][e & 7] = (bf16)pr;
+      dsf[2 * sub + (e >> 3)][e & 7] = (bf16)(pr * (dp[sub][e] - dmul * d4[sub][e >> 2][e & 3]) * dsmul);
+    };
+    bf16x8 a[64];
+    ld_rows(0);
+#pragma unroll
+    for (int t = 0; t < BW_PF; ++t) a[t] = ld(t);
+    s[0] = s[1] = dp[0] = dp[1] = floatx16{};
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int t = 0; t < 64; ++t) {
+      if (t + BW_PF < 64) a[t + BW_PF] = ld(t + BW_PF);
+      if (t < 32) {
+        const int sub = t >> 4, kk = (t & 15) >> 1;
+        if (t & 1) dp[sub] = mfma32x32x16(a[t], vf[kk], dp[sub]);
+        else s[sub] = mfma32x32x16(a[t], kf[kk], s[sub]);
+      } else {
+        const int u = t - 32, m = u >> 3, ds = (u >> 1) & 3;
+        if (u & 1) dk[ds] = mfma32x32x16(a[t], dsf[m], dk[ds]);
+        else dv[ds] = mfma32x32x16(a[t], pf[m], dv[ds]);
+      }
+      if (t == 16) ld_rows(1);
+      if (t >= 16 && t < 32) elem(0, t - 16);
+      if (t >= 32 && t < 48) elem(1, t - 32);
+      __builtin_amdgcn_sched_barrier(0);
+    }
     ATT_BARRIER();                                     // buffer n & 1 consumed
   }
 
