@@ -32,6 +32,9 @@
 // side).  K(t+1) is issued as soon as both waves finished reading K(t) and lands while
 // the softmax and PV of tile t run; V(t+1) is issued after PV(t) and lands during QK and
 // softmax of tile t+1.  The epilogue fuses the residual and the scatter to [B, S, H, D].
+// The exact tiles are visited in ascending new-KV order starting at a block that advances
+// with the launch index (a rotation of the list), so that the workgroups resident on one
+// XCD sweep the new KV together.
 #include "attn_tile.h"
 #include "icsa_kernels.h"
 
@@ -44,6 +47,9 @@
 #define SP_RESCALE_LOG2 8.0f
 #define SP_PF 2                          // MFMA operand read-ahead (steps); 3 spills at 256 VGPRs
 #define SP_DMA_PER_TILE 8                // LDS-DMA instructions per wave per K or V^T tile
+#ifndef SP_SWEEP_CONC
+#define SP_SWEEP_CONC 256                // sweep start advances NKV / SP_SWEEP_CONC per launch
+#endif
 
 // vmcnt waits: "all but the newest tile" / "everything".  Loads complete in issue order.
 #define SP_WAIT_OLDER() asm volatile("s_waitcnt vmcnt(8)" ::: "memory")
@@ -57,6 +63,7 @@ icsa_sparse_kernel(SparseParams p) {
   __shared__ __attribute__((aligned(16))) unsigned char vbuf[SP_BUF_BYTES];
   __shared__ int src_l[SP_MAX_TOPK];                  // source block of exact tile t (-1: zeros)
   __shared__ unsigned long long sel_l[SP_MAX_CHUNKS];  // selected new-KV blocks per chunk
+  __shared__ int rot_l;                               // exact tiles visited from list entry rot_l
 
   const int n_work = p.B * p.H * p.n_qblk;
   const int work = xcd_remap(blockIdx.x, n_work);
@@ -76,6 +83,12 @@ icsa_sparse_kernel(SparseParams p) {
 
   // ---- block lists: source blocks of the exact tiles, selection bitmask per chunk ----
   for (int c = tid; c < nc; c += SP_THREADS) sel_l[c] = 0ull;
+  if (tid == 0) rot_l = 0;
+  // Sweep start: the workgroups of one XCD (blockIdx.x % 8) launch in order and run at about
+  // the same pace, so starting the ascending list of launch w = blockIdx.x / 8 at new-KV
+  // block w * NKV / SP_SWEEP_CONC keeps the resident workgroups reading nearby blocks at the
+  // same time, shared in that XCD's L2.  Only the order of the online softmax changes.
+  const int sweep0 = (int)(((int64_t)(blockIdx.x / 8) * p.NKV / SP_SWEEP_CONC) % p.NKV);
   __syncthreads();
   {
     const int* idx_g = p.idx + ((int64_t)bh * p.n_qblk + slot) * top_k;
@@ -86,6 +99,7 @@ icsa_sparse_kernel(SparseParams p) {
       if (j >= 0 && j < p.NKV) {
         src = p.kvmap_identity ? j : kvmap[j];
         atomicOr(&sel_l[j >> 6], 1ull << (j & 63));
+        if (j < sweep0) atomicAdd(&rot_l, 1);
       }
       src_l[t] = src;
     }
@@ -111,7 +125,10 @@ icsa_sparse_kernel(SparseParams p) {
 #pragma unroll
   for (int m = 0; m < 4; ++m) vro[m] = v_lds_off(li, 2 * m + hl) * 2;
 
-  __syncthreads();                                    // src_l / sel_l ready
+  __syncthreads();                                    // src_l / sel_l / rot_l ready
+  const int rot = __builtin_amdgcn_readfirstlane(rot_l);
+  // list entry of exact tile g (the ascending list rotated to start at entry rot)
+  auto ex_entry = [&](int g) -> int { return g + rot < top_k ? g + rot : g + rot - top_k; };
 
   // Tile g: g < T1 exact block src_l[g]; T1 <= g < T2 pass-1 chunk g - T1 (K only);
   // g >= T2 pass-2 chunk g - T2.  issue_k returns the number of real key rows (the rest
@@ -122,7 +139,7 @@ icsa_sparse_kernel(SparseParams p) {
     int valid, rs2;                        // rs2: key row stride in bytes
     const bool ex = g < T1;
     if (ex) {
-      const int src = __builtin_amdgcn_readfirstlane(src_l[g]);
+      const int src = __builtin_amdgcn_readfirstlane(src_l[ex_entry(g)]);
       const int tok0 = src * ATT_BN;
       valid = src < 0 ? 0 : min(ATT_BN, p.Sk - tok0);
       base = kbase + (src < 0 ? 0 : (int64_t)tok0 * p.k_st);
@@ -152,7 +169,7 @@ icsa_sparse_kernel(SparseParams p) {
     int rs2;                               // V^T row stride in bytes
     const bool ex = g < T1;
     if (ex) {
-      const int src = __builtin_amdgcn_readfirstlane(src_l[g]);
+      const int src = __builtin_amdgcn_readfirstlane(src_l[ex_entry(g)]);
       zero = src < 0;
       base = vtbase + (zero ? 0 : (int64_t)src * ATT_BN);
       bytes = zero ? 0 : ((int64_t)(ICSA_D - 1) * p.vt_sd + ATT_BN) * 2;
