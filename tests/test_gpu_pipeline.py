@@ -101,3 +101,30 @@ def test_deterministic_and_linear_in_v(gpu):
     # decisions depend on q, k only; every stage is linear in v and x2 is exact in bf16/fp32
     x3 = editing_sparse_attention(q, k, 2 * v, t, t, alpha_2=0.5)
     assert torch.equal(x3, 2 * x1), "output not exactly linear in v"
+
+
+def test_batch2_packed_qkv_views(gpu):
+    # B = 2, q / k / v as strided views of one packed [B, S, 3, H, D] projection output
+    # (token stride 3 H D, head stride D), the layout a fused QKV GEMM produces
+    q, k, v, t = make_inputs(H=2, real=1024, pad=0, B=2, kind="random", seed=7)
+    qkv = torch.stack([q, k, v], dim=2)
+    qv, kv_, vv = qkv[:, :, 0], qkv[:, :, 1], qkv[:, :, 2]
+    assert not qv.is_contiguous() and qv.stride(1) == 3 * 2 * 128
+    x, _, _ = _run_case(gpu, qv, kv_, vv, t)
+    # each batch entry equals its own B = 1 call
+    for b in range(2):
+        xb, _ = _editing_sparse_attention_hip(q[b:b + 1].to(gpu), k[b:b + 1].to(gpu), v[b:b + 1].to(gpu), t, 0.7)
+        assert torch.equal(xb.cpu(), x[b:b + 1].cpu()), f"batch entry {b} differs from its B=1 call"
+
+
+@pytest.mark.parametrize("flat,srr,real", [(1.0, 0.01, 192), (0.0, 0.125, 1024)])
+def test_degenerate_splits(gpu, flat, srr, real):
+    # flat 1.0 with a tiny SRR: no diffuse blocks and no selected source blocks (the new KV is
+    # the target alone); flat 0.0: no peaked blocks, every block goes to the sparse kernel
+    q, k, v, t = make_inputs(H=2, real=real, pad=0, kind="random", seed=8)
+    _, views, info = _run_case(gpu, q, k, v, t, srr=srr, flat_ratio=flat)
+    z = info["sizes"]
+    if flat == 1.0:
+        assert z.n_diffuse == 0 and z.topK == 0
+    else:
+        assert z.n_peaked == 0 and z.topK > 0
