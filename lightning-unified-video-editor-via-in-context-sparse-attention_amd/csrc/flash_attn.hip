@@ -18,8 +18,10 @@
 // SIMD feeds the matrix pipe while the other keeps the vector ALU busy ("ping-pong").
 //
 // Tiles arrive by direct global->LDS buffer loads (LDS DMA: lane l of a load lands at
-// M0 + 16 l): K(k+1) and V(k) are issued in slot 2k and waited for at the end of slot
-// 2k+1, double buffered.  The LDS XOR swizzle is applied on the global side: each lane
+// M0 + 16 l), triple buffered.  Issuing LDS DMA blocks the issuing wave while the CU's
+// vector-memory path takes earlier requests, so only waves in their SOFT phase issue it,
+// one 1-KB segment between every 8 exponentials (group 1: K tiles, group 0: V^T tiles; the
+// slot schedule below).  The LDS XOR swizzle is applied on the global side: each lane
 // fetches the chunk that belongs in its LDS slot.  Per-lane global offsets are computed
 // once, the tile start is the scalar base of a buffer resource whose range covers only key
 // rows below Sk, and every LDS offset is hoisted out of the loop.
@@ -34,10 +36,12 @@
 #define FA_THREADS (FA_WAVES * 64)
 #define FA_QBLK_PER_WG (FA_WAVES / 2)
 #define FA_STAGE_BYTES (FA_WAVES * 32 * O_LDS_STRIDE * 4)    // epilogue staging, all waves
-#define FA_TILE_BYTES (2 * (K_TILE_BYTES + V_TILE_BYTES))
+#define FA_NBUF 3                                            // K and V^T tile buffers
+#define FA_TILE_BYTES (FA_NBUF * (K_TILE_BYTES + V_TILE_BYTES))
 #define FA_MAX_SEL 4096                                      // extra tiles (LDS list)
-#define FA_LDS_BYTES (FA_TILE_BYTES + 4 * FA_MAX_SEL > FA_STAGE_BYTES ? FA_TILE_BYTES + 4 * FA_MAX_SEL \
-                                                                    : FA_STAGE_BYTES)
+#define FA_JUNK_OFF (FA_TILE_BYTES + 4 * FA_MAX_SEL)         // landing area of disabled DMA
+#define FA_LOOP_BYTES (FA_JUNK_OFF + 4096)
+#define FA_LDS_BYTES (FA_LOOP_BYTES > FA_STAGE_BYTES ? FA_LOOP_BYTES : FA_STAGE_BYTES)
 #define FA_RESCALE_LOG2 8.0f
 #ifndef FA_PF
 #define FA_PF 3             // operand prefetch depth (MFMA steps)
@@ -76,18 +80,6 @@ icsa_flash_kernel(FlashParams p) {
   // ---- per-lane offsets, hoisted out of the loop ----
   const bf16* kb = p.k + (int64_t)b * p.k_sb + (int64_t)h * p.k_sh;
   const bf16* vb = p.vt + (int64_t)b * p.vt_sb + (int64_t)h * p.vt_sh;
-  // DMA segment s = 2 * wave + i (1 KB each): K rows 4s..4s+3, V^T rows 8s..8s+7.
-  int kvo[2], vvo[2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int s = 2 * wave + i;
-    const int kr = 4 * s + (lane >> 4), kp = lane & 15;          // LDS row / physical chunk
-    const int kc = kp ^ (kr & 15);                               // logical chunk in that slot
-    kvo[i] = (int)(((int64_t)kr * p.k_ss + 8 * kc) * 2);
-    const int vd = 8 * s + (lane >> 3), vp = lane & 7;
-    const int vc = vp ^ ((vd >> 1) & 7);
-    vvo[i] = (int)(((int64_t)vd * p.vt_sd + 8 * vc) * 2);
-  }
   int kro[8], vro[4];                                 // MFMA operand read offsets (bytes)
 #pragma unroll
   for (int kk = 0; kk < 8; ++kk) kro[kk] = k_lds_off(li, 2 * kk + hl) * 2;   // + 32 rows per sub-tile
@@ -97,40 +89,10 @@ icsa_flash_kernel(FlashParams p) {
   auto tile_tok0 = [&](int j) -> int {
     return j < p.n_tgt_tiles ? j * ATT_BN : __builtin_amdgcn_readfirstlane(sel_l[j - p.n_tgt_tiles]);
   };
-  auto kbuf = [&](int i) -> unsigned char* { return smem + i * K_TILE_BYTES; };
-  auto vbuf = [&](int i) -> unsigned char* { return smem + 2 * K_TILE_BYTES + i * V_TILE_BYTES; };
-  // DMA of K tile j into K buffer j & 1; the range covers only key rows below Sk.
-  // Returns the number of valid key rows (rows past it are zeroed by fill_tail).
-  auto issue_k = [&](int j) -> int {
-    const int tok0 = tile_tok0(j);
-    const int k_valid = min(ATT_BN, p.Sk - tok0);
-    const int64_t k_bytes = k_valid > 0 ? ((int64_t)(k_valid - 1) * p.k_ss + ICSA_D) * 2 : 0;
-    const __amdgpu_buffer_rsrc_t krs = make_rsrc(kb + (int64_t)tok0 * p.k_ss, k_bytes);
-    unsigned char* dst = kbuf(j & 1) + wave * 2048;
-#pragma unroll
-    for (int s = 0; s < 2; ++s)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (lds_ptr)(dst + 1024 * s), 16, kvo[s], 0, 0, 0);
-    return k_valid;
-  };
-  auto issue_v = [&](int j) {
-    const int tok0 = tile_tok0(j);
-    const __amdgpu_buffer_rsrc_t vrs =
-        make_rsrc(vb + tok0, ((int64_t)(ICSA_D - 1) * p.vt_sd + ATT_BN) * 2);
-    unsigned char* dst = vbuf(j & 1) + wave * 2048;
-#pragma unroll
-    for (int s = 0; s < 2; ++s)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (lds_ptr)(dst + 1024 * s), 16, vvo[s], 0, 0, 0);
-  };
-  // Zero key rows >= k_valid of this wave's own DMA segments (rows 8 w .. 8 w + 7), after
-  // its DMA completed, so padding keys are exact zeros.
-  auto fill_tail = [&](int j, int k_valid) {
-    if (k_valid >= ATT_BN) return;
-    const int row = 8 * wave + (lane >> 3);
-    if (row >= k_valid) {
-      unsigned char* dst = kbuf(j & 1) + row * ICSA_D * 2 + (lane & 7) * 32;
-      *reinterpret_cast<u32x4*>(dst) = u32x4{0u, 0u, 0u, 0u};
-      *reinterpret_cast<u32x4*>(dst + 16) = u32x4{0u, 0u, 0u, 0u};
-    }
+  // buffer of tile j
+  auto kbuf = [&](int j) -> unsigned char* { return smem + (j % FA_NBUF) * K_TILE_BYTES; };
+  auto vbuf = [&](int j) -> unsigned char* {
+    return smem + FA_NBUF * K_TILE_BYTES + (j % FA_NBUF) * V_TILE_BYTES;
   };
 
   floatx16 o[4] = {};
@@ -146,7 +108,7 @@ icsa_flash_kernel(FlashParams p) {
   auto gemm = [&](int k) {
     __builtin_amdgcn_s_setprio(1);              // the matrix-feeding wave wins issue ties
     if (k >= 1) {
-      const unsigned char* vs = vbuf((k - 1) & 1);
+      const unsigned char* vs = vbuf(k - 1);
       bf16x8 va[16];
 #pragma unroll
       for (int t = 0; t < FA_PF; ++t)
@@ -163,7 +125,7 @@ icsa_flash_kernel(FlashParams p) {
       }
     }
     if (k < n_tiles) {
-      const unsigned char* ks = kbuf(k & 1);
+      const unsigned char* ks = kbuf(k);
       bf16x8 ka[16];
       floatx16 acc0 = {}, acc1 = {};
 #pragma unroll
@@ -185,7 +147,51 @@ icsa_flash_kernel(FlashParams p) {
     }
     __builtin_amdgcn_s_setprio(0);
   };
-  // SOFT(k): mask, row max, lazy rescale, P(k)
+  // This wave's share (4 one-KB segments) of one tile's DMA, issued one segment at a time
+  // from inside the SOFT phase (see the slot schedule below).
+  const bool lag_w = group == 1;
+  const int dw = wave & 3;
+  int dofs[4];                            // segment offsets: K rows (group 1) / V^T rows (group 0)
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int sg = 4 * dw + i;
+    if (lag_w) {
+      const int kr = 4 * sg + (lane >> 4), kc = (lane & 15) ^ (kr & 15);
+      dofs[i] = (int)(((int64_t)kr * p.k_ss + 8 * kc) * 2);
+    } else {
+      const int vd = 8 * sg + (lane >> 3), vc = (lane & 7) ^ ((vd >> 1) & 7);
+      dofs[i] = (int)(((int64_t)vd * p.vt_sd + 8 * vc) * 2);
+    }
+  }
+  __amdgpu_buffer_rsrc_t dma_rs = make_rsrc(kb, 0);
+  unsigned char* dma_dst = smem;
+  bool dma_on = false;
+  int dma_kvalid = ATT_BN;
+  // sets up this wave's part of tile j: K(j) for group 1, V^T(j) for group 0
+  auto dma_setup = [&](int j) {
+    dma_on = j < n_tiles;
+    if (!dma_on) {                        // issue stays branch-free: an empty range, junk LDS
+      dma_rs = make_rsrc(kb, 0);
+      dma_dst = smem + FA_JUNK_OFF;
+      return;
+    }
+    const int tok0 = tile_tok0(j);
+    if (lag_w) {
+      const int k_valid = min(ATT_BN, p.Sk - tok0);
+      const int64_t k_bytes = k_valid > 0 ? ((int64_t)(k_valid - 1) * p.k_ss + ICSA_D) * 2 : 0;
+      dma_rs = make_rsrc(kb + (int64_t)tok0 * p.k_ss, k_bytes);
+      dma_dst = kbuf(j) + dw * 4096;
+      dma_kvalid = k_valid;
+    } else {
+      dma_rs = make_rsrc(vb + tok0, ((int64_t)(ICSA_D - 1) * p.vt_sd + ATT_BN) * 2);
+      dma_dst = vbuf(j) + dw * 4096;
+    }
+  };
+  auto dma_seg = [&](int i) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(dma_rs, (lds_ptr)(dma_dst + 1024 * i), 16, dofs[i], 0, 0, 0);
+  };
+  // SOFT(k): mask, row max, lazy rescale, P(k); the wave's DMA segments go out one at a time
+  // between the exponentials
   auto soft = [&](int k) {
     const int mask_from = k < p.n_tgt_tiles ? p.t_limit - k * ATT_BN : ATT_BN;
     if (mask_from < ATT_BN) {
@@ -214,57 +220,99 @@ icsa_flash_kernel(FlashParams p) {
     }
     float rs = 0.f;
 #pragma unroll
-    for (int sub = 0; sub < 2; ++sub)
+    for (int sb = 0; sb < 2; ++sb)
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const float e = __builtin_amdgcn_exp2f(fmaf(s[sub][i], c, -m_ref));
+        if ((i & 7) == 0) {                // DMA segment 2 sb + i / 8 before every 8th exponential
+          __builtin_amdgcn_sched_barrier(0);
+          dma_seg(2 * sb + (i >> 3));
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        const float e = __builtin_amdgcn_exp2f(fmaf(s[sb][i], c, -m_ref));
         rs += e;
-        pf[2 * sub + (i >> 3)][i & 7] = (bf16)e;
+        pf[2 * sb + (i >> 3)][i & 7] = (bf16)e;
       }
     l_run += rs;
   };
 
-  // Slot schedule.  Slot t ends with a workgroup barrier.  issue(k) = DMA of K(k+1) and
-  // V(k), started at the beginning of slot 2k and waited for at the end of slot 2k+1.
-  // Both groups run the same loop body  [GEMM(k) | barrier | SOFT(k) | barrier]:  group 0
-  // in slots (2k, 2k+1), group 1 one slot later (2k+1, 2k+2) -- it enters with one extra
-  // barrier and group 0 leaves with one, so the barrier counts match.  Only the DMA
-  // issue / wait points differ between the groups.
+  // Slot schedule.  Every slot ends with a workgroup barrier; group 0 runs GEMM(k) in slot
+  // 2k and SOFT(k) in slot 2k + 1, group 1 one slot later.  Issuing LDS-DMA blocks the
+  // issuing wave while the CU's vector-memory path drains earlier requests (about 22
+  // s_memtime ticks per 1-KB instruction), so the tile DMA is issued only by waves in their
+  // SOFT phase, one segment between every 8 exponentials, never by a GEMM wave:
+  //   K(j): group 1 during SOFT(j - 3), slot 2j - 4; waited for by group 1 at the end of its
+  //         GEMM(j - 1), slot 2j - 1; read in slots 2j (group 0) and 2j + 1 (group 1);
+  //   V(j): group 0 during SOFT(j - 1), slot 2j - 1; waited for by group 0 at the end of its
+  //         SOFT(j), slot 2j + 1; read (as PV(j)) in slots 2j + 2 and 2j + 3.
+  // Three buffers per kind: K(j) overwrites K(j - 3), last read in slot 2j - 5; V(j)
+  // overwrites V(j - 3), last read (PV(j - 3)) in slot 2j - 3.  Loads complete
+  // in issue order, so vmcnt(4) waits for all but this wave's newest tile.  Slots past the
+  // last tile issue empty-range loads into a junk LDS area (the issue stays branch-free).
   const bool compute = q_valid > 0;
   const bool lag = group == 1;
-  auto issue = [&](int k) -> int {
-    int kv_next = ATT_BN;
-    if (k + 1 < n_tiles) kv_next = issue_k(k + 1);
-    if (k < n_tiles) issue_v(k);
-    return kv_next;
+  auto wait_tile = [&](bool newer) {
+    if (newer) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   };
-  auto wait_fill = [&](int k, int kv_next) {       // completes issue(k)
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    if (k + 1 < n_tiles) fill_tail(k + 1, kv_next);
+  // zero key rows >= k_valid of a group-1 wave's K segments (rows 16 dw .. 16 dw + 15)
+  auto fill_tail4 = [&](int j, int k_valid) {
+    if (k_valid >= ATT_BN) return;
+    const int row = 16 * dw + (lane >> 2);
+    if (row >= k_valid) {
+      unsigned char* dst = kbuf(j) + row * ICSA_D * 2 + (lane & 3) * 64;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) *reinterpret_cast<u32x4*>(dst + 16 * e) = u32x4{0u, 0u, 0u, 0u};
+    }
   };
-
-  {
-    const int kv0 = issue_k(0);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    fill_tail(0, kv0);
+  auto issue_all = [&]() {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dma_seg(i);
+  };
+  // prologue: group 1 issues K(0), K(1); group 0 issues V(0); K(0) is made visible
+  int kv_a = ATT_BN, kv_b = ATT_BN;       // group 1: valid rows of K(k + 1) and K(k + 2)
+  if (lag) {
+    dma_setup(0);
+    const int kv0 = dma_kvalid;
+    issue_all();
+    dma_setup(1);
+    kv_a = dma_kvalid;
+    issue_all();
+    wait_tile(1 < n_tiles);
+    fill_tail4(0, kv0);
+  } else {
+    dma_setup(0);
+    issue_all();
   }
-  __syncthreads();
-  int kv_pending = ATT_BN;
-  if (lag) {                       // slot 0 for group 1: issue(0), then its first barrier
-    kv_pending = issue(0);
+  ATT_BARRIER();
+  if (lag) {                               // slot 0 for group 1: K(2) ("SOFT(-1)")
+    dma_setup(2);
+    kv_b = dma_kvalid;
+    issue_all();
     ATT_BARRIER();
   }
   for (int k = 0; k <= n_tiles; ++k) {
-    if (!lag) kv_pending = issue(k);            // slot 2k starts
     if (compute) gemm(k);
-    if (lag) wait_fill(k, kv_pending);          // end of slot 2k+1 (group 1 view)
+    // group 1, end of slot 2k + 1: K(k + 1) (K(k + 2) is newer when it exists)
+    if (lag && k + 1 < n_tiles) {
+      wait_tile(k + 2 < n_tiles);
+      fill_tail4(k + 1, kv_a);
+    }
     ATT_BARRIER();
-    if (lag) kv_pending = issue(k + 1);         // slot 2k+2 starts (group 1 view)
+    // SOFT(k): group 0 issues V(k + 1), group 1 issues K(k + 3)
+    dma_setup(lag ? k + 3 : k + 1);
+    const int kv_new = dma_kvalid;
     if (compute && k < n_tiles) soft(k);
-    if (!lag) wait_fill(k, kv_pending);         // end of slot 2k+1 (group 0 view)
+    else issue_all();
+    // group 0, end of slot 2k + 1: V(k) (V(k + 1) is newer when it exists)
+    if (!lag && k < n_tiles) wait_tile(k + 1 < n_tiles);
+    if (lag) { kv_a = kv_b; kv_b = kv_new; }
     ATT_BARRIER();
   }
   if (!lag) ATT_BARRIER();       // group 0's extra slot
+  // empty-range DMA of the last slots may still be in flight towards the junk area, which
+  // the output staging below overlaps
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
 
   // ---- epilogue: 1/l, residual, scatter (the workgroup owns the CU's LDS: one round) ----
   float* o_lds = reinterpret_cast<float*>(smem) + wave * 32 * O_LDS_STRIDE;
