@@ -47,6 +47,18 @@ def test_flash_attn_dense(gpu, Sq, Sk, H):
     compare_out(out, ref)
 
 
+@pytest.mark.parametrize("Sk", [65, 128, 129, 191, 192])
+def test_flash_attn_few_tiles(gpu, Sk):
+    # 2-3 key tiles, full and partial: the schedule's prologue (K(0), K(1), V(0)), its
+    # empty-range DMA of the slots past the last tile and the zero fill of the partial tile
+    print(f"[case] flash few tiles Sk={Sk}", flush=True)
+    q, k, v = _bf16(1, 320, 2, 128, seed=11), _bf16(1, Sk, 2, 128, seed=12), _bf16(1, Sk, 2, 128, seed=13)
+    out = flash_attn_func(q.to(gpu), k.to(gpu), v.to(gpu), out_dtype=torch.float32)
+    ref = O.dense_attention(q.double().permute(0, 2, 1, 3), k.double().permute(0, 2, 1, 3),
+                            v.double().permute(0, 2, 1, 3)).permute(0, 2, 1, 3)
+    compare_out(out, ref)
+
+
 def test_flash_attn_large_logits(gpu):
     # peaked softmax: logits up to ~40 exercise the running-max rescale path
     q, k, v = _bf16(1, 512, 2, 128, seed=7, scale=3.0), _bf16(1, 1024, 2, 128, seed=8, scale=3.0), \
