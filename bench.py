@@ -61,6 +61,9 @@ def load_traffic(path):
     return None
 
 
+CPU_SHARE = 16
+
+
 def cpu_baseline(seconds, H_full=40):
     """The float32 CPU oracle on a bounded sample of the benchmark's own workload: one head
     of configuration 2 (B=1, S=65,536, t=32,768, D=128).  Every stage of the path works per
@@ -70,12 +73,15 @@ def cpu_baseline(seconds, H_full=40):
     reference's own CPU-runnable case) is timed beside it for continuity."""
     import torch
     import oracle as O
-    from in_context_sparse_attention.synthetic import config_inputs, make_inputs
+    from icsa_hip.synthetic import config_inputs, make_inputs
+    host_cpus = os.cpu_count() or 1
     try:
-        cores = len(os.sched_getaffinity(0))
+        affinity = len(os.sched_getaffinity(0))
     except AttributeError:
-        cores = os.cpu_count() or 1
-    cores = max(1, min(cores, 16))
+        affinity = host_cpus
+    # The GPU box grants one GPU's job a 16-core share of the host, whatever the affinity
+    # mask shows, so the oracle runs on at most 16 threads.
+    cores = max(1, min(affinity, CPU_SHARE))
     torch.set_num_threads(cores)
 
     def median_time(q32, k32, v32, t, budget, min_runs):
@@ -100,6 +106,10 @@ def cpu_baseline(seconds, H_full=40):
         "value": 4.0 * B * H_full * S * S * D / layer_s / 1e12,
         "unit": "TFLOP/s (dense-equivalent)",
         "cores": torch.get_num_threads(),
+        "host_cpu_count": host_cpus,
+        "affinity_cores": affinity,
+        "threads_note": (f"{torch.get_num_threads()} threads: the GPU box's CPU share for one GPU "
+                         f"is {CPU_SHARE} cores (os.cpu_count() {host_cpus}, affinity {affinity})"),
         "kind": "port",
         "sample": (f"one head of config 2 (B=1, S={S}, t={t}, D={D}) through the whole path in fp32, "
                    f"{n} runs, median {med:.2f} s per head; layer = {H_full} heads = {layer_s:.1f} s"),
@@ -153,7 +163,7 @@ def wan_attention_bench(steps, warmup, log_fn):
     attention output, (a) through this build's fused producer + attention core and (b)
     through the reference's glue (fp32 RMSNorm, float64 RoPE) feeding the same attention."""
     import torch
-    from in_context_sparse_attention import editing_sparse_attention, wan
+    from icsa_hip import editing_sparse_attention, wan
     dev = torch.device("cuda:0")
     B, H, D = 1, 40, 128
     grid = (21, 30, 52)
@@ -223,14 +233,14 @@ def block_bench(steps, warmup, log_fn):
     cross_attn_norm) over 65,520 tokens (21x30x52 target + source grids), cross attention to
     512 text tokens, bf16 random-init weights (the reference's init_weights scheme), adaLN
     time embedding of t ~ U(0, 1000).  Timed: (a) the HIP block
-    (in_context_sparse_attention.wan.WanAttentionBlock); (b) the same parameters through the
+    (icsa_hip.wan.WanAttentionBlock); (b) the same parameters through the
     reference's PyTorch glue (LayerNorm / modulation / residual in fp32, WanRMSNorm, float64
     RoPE, fp32 q / k into the attention path), with the same attention kernels."""
     import math as _m
     import torch
     import torch.nn as nn
     import torch.nn.functional as F
-    from in_context_sparse_attention import editing_sparse_attention, flash_attn_func, wan
+    from icsa_hip import editing_sparse_attention, flash_attn_func, wan
     dev = torch.device("cuda:0")
     dim, H, ffn, L, text_dim, freq_dim = 5120, 40, 13824, 512, 4096, 256
     D = dim // H
@@ -343,7 +353,7 @@ def dit_step_bench(steps, log_fn):
     prompt, 512 text tokens of dim 4096 each); the guidance combination is included, the
     scheduler update (an elementwise step on the latent) is not."""
     import torch
-    from in_context_sparse_attention import wan
+    from icsa_hip import wan
     dev = torch.device("cuda:0")
     torch.manual_seed(0)
     prev = torch.get_default_dtype()
@@ -395,8 +405,8 @@ def sparse_bwd_bench(steps, warmup, log_fn):
     interval chunk (triton_kernels.py:330-475): BH * NQ * (top_k * 5 * 2*64*64*128 +
     5 * 2*64*NKVp*128)."""
     import torch
-    from in_context_sparse_attention import (sparse_piecewise_attn_1st_intervals_bwd_hip,
-                                             sparse_piecewise_attn_1st_intervals_fwd_hip)
+    from icsa_hip import (sparse_piecewise_attn_1st_intervals_bwd_hip,
+                          sparse_piecewise_attn_1st_intervals_fwd_hip)
     dev = torch.device("cuda:0")
     B, H, TQ, TKV, D, sar = 1, 40, 32768, 36864, 128, 0.0625
     g = torch.Generator(device=dev).manual_seed(0)
@@ -485,10 +495,10 @@ def main():
         sys.exit(2)
 
     import torch
-    from in_context_sparse_attention import _lib, flash_attn_func, gather_kv
-    from in_context_sparse_attention.editing_sparse_attention import (
+    from icsa_hip import _lib, flash_attn_func, gather_kv
+    from icsa_hip.editing_sparse_attention import (
         _editing_sparse_attention_hip, derived_sizes)
-    from in_context_sparse_attention.synthetic import config_inputs
+    from icsa_hip.synthetic import config_inputs
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)

@@ -1,6 +1,9 @@
-"""MI355X (gfx950) in-context sparse attention -- the reference package's API with a HIP backend.
+"""icsa_hip: MI355X (gfx950) in-context sparse attention, the reference package's API with a
+HIP backend.
 
-Mirrors ``in_context_sparse_attention/__init__.py`` of the reference (``Backend``,
+The package has its own name so that the reference's ``in_context_sparse_attention``
+package can import it (its ``backend='hip'`` branch).  It mirrors that package's
+``__init__.py`` (``Backend``,
 ``editing_sparse_attention``, ``editing_sparse_attention_tilelang``) and adds the kernel-host
 functions of the HIP backend.  Importing does not load the native library; the first GPU
 call does, and fails loudly if ``libicsa.so`` has not been built.

@@ -167,7 +167,7 @@ def lib():
             if not os.path.exists(_LIB_PATH):
                 raise OSError(
                     f"libicsa.so not found at {_LIB_PATH}; build it with "
-                    "`python -m in_context_sparse_attention.build` (hipcc, gfx950)")
+                    "`python -m icsa_hip.build` (hipcc, gfx950)")
             handle = ctypes.CDLL(_LIB_PATH)
             for name, (res, args) in _SIGNATURES.items():
                 fn = getattr(handle, name)

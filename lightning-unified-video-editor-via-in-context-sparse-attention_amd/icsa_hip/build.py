@@ -1,9 +1,9 @@
 """Build ``libicsa.so`` (gfx950) from ``../csrc`` with hipcc.
 
 Every HIP source is compiled to an object in ``csrc/_build`` (in parallel), then linked
-into ``in_context_sparse_attention/libicsa.so`` next to this file.  The link goes to a
+into ``icsa_hip/libicsa.so`` next to this file.  The link goes to a
 temporary name first and is renamed into place, so a concurrent loader never sees a
-half-written library.  Run ``python -m in_context_sparse_attention.build`` or call
+half-written library.  Run ``python -m icsa_hip.build`` or call
 :func:`build_library`.
 """
 from __future__ import annotations

@@ -2,14 +2,17 @@
 
 Mirror of the reference's ``in_context_sparse_attention/editing_sparse_attention.py``:
 ``Backend`` (:25-34) gains ``HIP = 'hip'``, and ``editing_sparse_attention`` (:67-232) keeps
-its signature.  With ``backend='hip'`` the whole path -- pooling, compressed attention,
-per-head source retrieval, peaked/diffuse split, flash attention for the peaked blocks,
-sparse piecewise attention for the diffuse blocks, scatter and residual -- runs as one
-launch sequence of hand-written gfx950 kernels (libicsa.so) on the current stream; the
-concatenated new KV, the broadcast out_c and the gathered query halves are never built.
+its signature, including the default ``backend='tilelang'``.  With ``backend='hip'`` the
+whole path -- pooling, compressed attention, per-head source retrieval, peaked/diffuse
+split, flash attention for the peaked blocks, sparse piecewise attention for the diffuse
+blocks, scatter and residual -- runs as one launch sequence of hand-written gfx950 kernels
+(libicsa.so) on the current stream; the concatenated new KV, the broadcast out_c and the
+gathered query halves are never built.
 
-The TileLang and Triton backends are CUDA-only and are not part of this build: naming
+The TileLang and Triton backends are CUDA-only and are not part of this package: naming
 them passes ``Backend.validate`` (they are valid names) but raises ``NotImplementedError``.
+The reference's module keeps serving them; it dispatches ``backend='hip'`` here through
+the few lines its integration patch adds.
 """
 from __future__ import annotations
 
@@ -18,8 +21,8 @@ import ctypes
 import torch
 
 from . import _lib
-from .hip_host import (BLOCK_M, IcsaArgumentError, _require, dtype_code, inner_contiguous,
-                       ptr, stream_ptr)
+from .hip_host import (BLOCK_M, IcsaArgumentError, _require, check_index_lists, dtype_code,
+                       inner_contiguous, ptr, stream_ptr)
 
 
 class Backend:
@@ -103,11 +106,15 @@ def _editing_sparse_attention_hip(q, k, v, t_seq_len, alpha_2=1.0, SPARSITY_RATI
     a, a_scalar, a_dt, a_st = _alpha_view(alpha_2, B, S, H, D, q.device)
     inject = inject or {}
     inj = {}
-    for name, shape in (("sel", (B, H, sizes["topK"])), ("order", (B, H, sizes["NB"])),
-                        ("l3", (B, H, sizes["n_diffuse"], sizes["top_k"]))):
+    # injected decisions (a testing hook): the kernels index q rows with `order`, source
+    # blocks with `sel` and new-KV blocks with `l3`, so their ranges are checked here
+    for name, shape, hi in (("sel", (B, H, sizes["topK"]), sizes["n_s"]),
+                            ("order", (B, H, sizes["NB"]), sizes["NB"]),
+                            ("l3", (B, H, sizes["n_diffuse"], sizes["top_k"]), sizes["NKV"])):
         if inject.get(name) is not None:
             t = inject[name].to(device=q.device, dtype=torch.int32).contiguous()
             _require(tuple(t.shape) == shape, f"inject[{name!r}] must have shape {shape}")
+            check_index_lists(t, hi, f"inject[{name!r}]")
             inj[name] = t
     ev_args = []
     fn = L.icsa_editing_sparse_attention
@@ -165,7 +172,7 @@ def workspace_views(ws: torch.Tensor, offs, sizes: dict, B: int, H: int, D: int)
 
 
 def editing_sparse_attention(q, k, v, t_seq_len, s_seq_len, alpha_2=1.0, alpha_3=1.0,
-                             SPARSITY_RATIO=0.0625, backend=Backend.HIP, *, srr=0.125,
+                             SPARSITY_RATIO=0.0625, backend=Backend.TILELANG, *, srr=0.125,
                              flat_ratio=0.5):
     """Editing sparse attention (reference: editing_sparse_attention.py:67-232).
 
@@ -177,7 +184,8 @@ def editing_sparse_attention(q, k, v, t_seq_len, s_seq_len, alpha_2=1.0, alpha_3
             broadcastable to [B, S, H, D])
         alpha_3: unused (API compatibility)
         SPARSITY_RATIO: fraction of KV blocks for the exact top-k (also sets k_sparsity)
-        backend: 'hip' (this build); 'tilelang' / 'triton' raise NotImplementedError
+        backend: 'hip' runs this build; 'tilelang' (the reference's default) and 'triton'
+            raise NotImplementedError here
         srr: source retrieval ratio (reference: 1/8, ``n_s // 8``)
         flat_ratio: fraction of query blocks given exact attention (reference: 1/2)
 
@@ -193,7 +201,8 @@ def editing_sparse_attention(q, k, v, t_seq_len, s_seq_len, alpha_2=1.0, alpha_3
     return x
 
 
-# Backward-compatible alias of the reference (there: always tilelang; here: the HIP path).
+# Backward-compatible alias of the reference (editing_sparse_attention.py:235-236): the same
+# function with the same default backend.
 editing_sparse_attention_tilelang = editing_sparse_attention
 
 __all__ = ["Backend", "editing_sparse_attention", "editing_sparse_attention_tilelang",

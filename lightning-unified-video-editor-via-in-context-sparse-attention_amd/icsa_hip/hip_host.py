@@ -48,6 +48,22 @@ def inner_contiguous(t: torch.Tensor) -> torch.Tensor:
     return t if ok else t.contiguous()
 
 
+def check_index_lists(idx: torch.Tensor, hi: int, name: str, allow_neg: bool = False,
+                      distinct: bool = True) -> None:
+    """Host check of a caller-supplied index list (last dim): entries in ``[0, hi)`` (or -1
+    where ``allow_neg``), distinct within each row.  The kernels index device memory with
+    these values, so a bad list must be refused before the call, not read out of bounds."""
+    if idx.numel() == 0:
+        return
+    x = idx.long()
+    lo_ok = (x >= -1) if allow_neg else (x >= 0)
+    _require(bool((lo_ok & (x < hi)).all()), f"{name}: entries must lie in [{'-1' if allow_neg else '0'}, {hi})")
+    if distinct and x.shape[-1] > 1:
+        srt = torch.sort(x, dim=-1).values
+        dup = (srt[..., 1:] == srt[..., :-1]) & (srt[..., 1:] >= 0)
+        _require(not bool(dup.any()), f"{name}: entries must be distinct within each list")
+
+
 def stream_ptr(device: torch.device) -> ctypes.c_void_p:
     return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
 
@@ -101,6 +117,7 @@ def sparse_piecewise_attn_1st_intervals_hip(q: torch.Tensor, k: torch.Tensor, v:
     if indices is not None:
         inj = indices.to(device=q.device, dtype=torch.int32).contiguous()
         _require(tuple(inj.shape) == (B, H, NQ, top_k), f"indices must be [B, H, {NQ}, {top_k}]")
+        check_index_lists(inj, NKV, "indices")
     idx_out = torch.empty(B, H, NQ, top_k, dtype=torch.int32, device=q.device) if return_indices else None
     rc = L.icsa_sparse_piecewise_attn(
         ptr(q), q.stride(0), q.stride(1), q.stride(2),
@@ -158,6 +175,7 @@ def sparse_piecewise_attn_1st_intervals_fwd_hip(q, k, v, sparsity: float = 0.1, 
     if indices is not None:
         inj = indices.to(device=q.device, dtype=torch.int32).contiguous()
         _require(tuple(inj.shape) == (B, H, NQ, top_k), f"indices must be [B, H, {NQ}, {top_k}]")
+        check_index_lists(inj, NKV, "indices")
     rc = L.icsa_sparse_piecewise_attn_fwd(
         ptr(q), q.stride(0), q.stride(1), q.stride(2),
         ptr(k), k.stride(0), k.stride(1), k.stride(2),
@@ -171,12 +189,16 @@ def sparse_piecewise_attn_1st_intervals_fwd_hip(q, k, v, sparsity: float = 0.1, 
 
 
 @torch.no_grad()
-def sparse_piecewise_attn_1st_intervals_bwd_hip(do, q, k, v, out, lse, indices, grad_dtype=None):
+def sparse_piecewise_attn_1st_intervals_bwd_hip(do, q, k, v, out, lse, indices, grad_dtype=None,
+                                                check_indices=True):
     """Gradients ``(dq, dk, dv)`` of the sparse piecewise attention, as
     SparsePiecewiseAttn1stIntervalsFunction.backward (triton_kernels.py:541-598) computes
     them from the saved (q, k, v, out, lse, indices), without atomics (the same inputs give
     the same bits).  ``grad_dtype``: bf16 (default: q.dtype, as the reference's final cast)
-    or float32."""
+    or float32.  ``indices`` must hold distinct blocks in ``[0, TKV/64)`` per query block
+    (the forward's top-k always does; the reference's atomics would count a repeated entry
+    twice in every gradient, this build's key-major dk / dv pass once), which
+    ``check_indices`` verifies on the host (one device sync)."""
     _check_sparse_args(q, k, v, 64)
     B, H, TQ, D = q.shape
     TKV = k.shape[2]
@@ -194,6 +216,8 @@ def sparse_piecewise_attn_1st_intervals_bwd_hip(do, q, k, v, out, lse, indices, 
     lse = lse.contiguous()
     idx = indices.to(dtype=torch.int32).contiguous()
     top_k = idx.shape[-1]
+    if check_indices:
+        check_index_lists(idx, TKV // BLOCK_M, "indices")
     L = _lib.lib()
     dq = torch.empty(B, H, TQ, D, dtype=gd, device=q.device)
     dk = torch.empty(B, H, TKV, D, dtype=gd, device=q.device)
@@ -235,7 +259,7 @@ class SparsePiecewiseAttn1stIntervalsFunction(torch.autograd.Function):
     def backward(ctx, do):
         q, k, v, out, lse, idx = ctx.saved_tensors
         dq, dk, dv = sparse_piecewise_attn_1st_intervals_bwd_hip(
-            do.to(torch.bfloat16), q, k, v, out, lse, idx)
+            do.to(torch.bfloat16), q, k, v, out, lse, idx, check_indices=False)
         return dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), None, None
 
 

@@ -193,7 +193,7 @@ def pool_blocks(x: torch.Tensor, dtype=torch.float64):
     NB = ceil_div(S, BLOCK_M)
     xp = F.pad(x.to(dtype), (0, 0, 0, 0, 0, NB * BLOCK_M - S))
     sums = xp.view(B, NB, BLOCK_M, H, D).sum(2).permute(0, 2, 1, 3).contiguous()
-    sizes = block_sizes(S).to(dtype)
+    sizes = block_sizes(S).to(device=x.device, dtype=dtype)
     means = sums / sizes.view(1, 1, -1, 1)
     return sums, means
 
@@ -233,9 +233,10 @@ def new_kv_token_map(t: int, S: int, sel: torch.Tensor) -> torch.Tensor:
     """
     B, H, topK = sel.shape
     n_t = t // BLOCK_M
-    tgt = torch.arange(t, dtype=torch.int64).view(1, 1, t).expand(B, H, t)
+    dev = sel.device
+    tgt = torch.arange(t, dtype=torch.int64, device=dev).view(1, 1, t).expand(B, H, t)
     src = (n_t * BLOCK_M + sel.long()[..., None] * BLOCK_M
-           + torch.arange(BLOCK_M, dtype=torch.int64)).reshape(B, H, topK * BLOCK_M)
+           + torch.arange(BLOCK_M, dtype=torch.int64, device=dev)).reshape(B, H, topK * BLOCK_M)
     src = torch.where(src < S, src, torch.full_like(src, -1))
     return torch.cat([tgt, src], dim=-1)
 
@@ -272,7 +273,7 @@ def dense_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     editing_sparse_attention.py:211-215), chunked over queries to bound memory."""
     D = q.shape[-1]
     outs = []
-    kt = k.transpose(-2, -1)
+    kt = k.transpose(-2, -1).contiguous()
     for s0 in range(0, q.shape[-2], chunk):
         s = torch.matmul(q[..., s0:s0 + chunk, :], kt) / math.sqrt(D)
         outs.append(torch.matmul(torch.softmax(s, dim=-1), v))
@@ -309,37 +310,38 @@ def sparse_piecewise_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     TKV = k.shape[2]
     assert TQ % BLOCK_M == 0 and TKV % BLOCK_M == 0
     NQ, NKV = TQ // BLOCK_M, TKV // BLOCK_M
+    dev = q.device              # every intermediate follows the inputs' device
     scale = 1.0 / math.sqrt(D)
     qd, kd, vd = q.to(dtype), k.to(dtype), v.to(dtype)
     QC = qd.view(B, H, NQ, BLOCK_M, D).sum(3)
     KC = kd.view(B, H, NKV, BLOCK_M, D).sum(3)
     VC = vd.view(B, H, NKV, BLOCK_M, D).sum(3)
-    scores = torch.matmul(QC, KC.transpose(-2, -1))
+    scores = torch.matmul(QC, KC.transpose(-2, -1).contiguous())
     top_k = max(1, int(sparsity * NKV))
     if indices is None:
         indices = ranked_topk(scores, top_k)
-    indices = torch.sort(indices.long(), dim=-1).values
+    indices = torch.sort(indices.long().to(dev), dim=-1).values
     assert indices.shape == (B, H, NQ, top_k)
     n_chunks = ceil_div(NKV, BN_INTERVAL)
     kb = kd.view(B, H, NKV, BLOCK_M, D)
     vb = vd.view(B, H, NKV, BLOCK_M, D)
-    out = torch.empty(B, H, TQ, D, dtype=dtype)
-    lse = torch.empty(B, H, TQ, dtype=dtype)
-    bi = torch.arange(B).view(B, 1, 1, 1)
-    hi = torch.arange(H).view(1, H, 1, 1)
+    out = torch.empty(B, H, TQ, D, dtype=dtype, device=dev)
+    lse = torch.empty(B, H, TQ, dtype=dtype, device=dev)
+    bi = torch.arange(B, device=dev).view(B, 1, 1, 1)
+    hi = torch.arange(H, device=dev).view(1, H, 1, 1)
     for n0 in range(0, NQ, qchunk):
         n1 = min(NQ, n0 + qchunk)
         qb = qd[:, :, n0 * BLOCK_M:n1 * BLOCK_M].view(B, H, n1 - n0, BLOCK_M, D)
         idx = indices[:, :, n0:n1]
         kx = kb[bi, hi, idx].reshape(B, H, n1 - n0, top_k * BLOCK_M, D)
         vx = vb[bi, hi, idx].reshape(B, H, n1 - n0, top_k * BLOCK_M, D)
-        s_ex = torch.matmul(qb, kx.transpose(-2, -1)) * scale
+        s_ex = torch.matmul(qb, kx.transpose(-2, -1).contiguous()) * scale
         m = s_ex.max(-1).values
         p = torch.exp(s_ex - m[..., None])
         l = p.sum(-1)
         acc = torch.matmul(p, vx)
-        s_int = torch.matmul(qb, KC[:, :, None].transpose(-2, -1)) * (scale / BLOCK_M)
-        selected = torch.zeros(B, H, n1 - n0, NKV, dtype=torch.bool)
+        s_int = torch.matmul(qb, KC[:, :, None].transpose(-2, -1).contiguous()) * (scale / BLOCK_M)
+        selected = torch.zeros(B, H, n1 - n0, NKV, dtype=torch.bool, device=dev)
         selected.scatter_(-1, idx, True)
         s_int = s_int.masked_fill(selected[:, :, :, None, :], -math.inf)
         g_acc = torch.zeros_like(acc)
@@ -387,7 +389,8 @@ def editing_sparse_attention(q, k, v, t_seq_len: int, s_seq_len: int, alpha_2=1.
     """
     B, S, H, D = q.shape
     sz = derive_sizes(B, S, H, D, t_seq_len, SPARSITY_RATIO, srr, flat_ratio)
-    decisions = decisions or {}
+    decisions = {k_: v_.to(q.device) for k_, v_ in (decisions or {}).items() if v_ is not None}
+    dev = q.device              # every intermediate follows the inputs' device
     qs, qc = pool_blocks(q, dtype)
     ks, kc = pool_blocks(k, dtype)
     vs, vc = pool_blocks(v, dtype)
@@ -406,9 +409,9 @@ def editing_sparse_attention(q, k, v, t_seq_len: int, s_seq_len: int, alpha_2=1.
     NB = sz.NB
     qpad = F.pad(q.to(dtype), (0, 0, 0, 0, 0, NB * BLOCK_M - S)).permute(0, 2, 1, 3)
     qblk = qpad.reshape(B, H, NB, BLOCK_M, D)
-    bi = torch.arange(B).view(B, 1, 1)
-    hi = torch.arange(H).view(1, H, 1)
-    out_blk = torch.zeros(B, H, NB, BLOCK_M, D, dtype=dtype)
+    bi = torch.arange(B, device=dev).view(B, 1, 1)
+    hi = torch.arange(H, device=dev).view(1, H, 1)
+    out_blk = torch.zeros(B, H, NB, BLOCK_M, D, dtype=dtype, device=dev)
 
     l3 = None
     l3_scores = None

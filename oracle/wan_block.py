@@ -58,18 +58,19 @@ def layer_norm(x, eps, w=None, b=None):
 
 
 def wan_block_forward(P: dict, x, e, context, grid, src_grid, tag, freqs, num_heads, eps=1e-6,
-                      decisions=None, sparsity=0.0625, x_is_bf16=False):
+                      decisions=None, sparsity=0.0625, x_is_bf16=False, device="cpu"):
     """One block on float64 tensors.  P: the block's state dict (reference parameter names).
     x [B, S, dim], e [B, 6, dim], context [B, L, dim].  ``x_is_bf16``: the block input is the
     bf16 patch embedding (the model's first block), so norm1's ``.type_as(x)`` rounds the
-    LayerNorm to bf16.  Returns (x, path-oracle info)."""
+    LayerNorm to bf16.  ``device``: where the float64 arithmetic runs (the same operations
+    on either device).  Returns (x, path-oracle info)."""
     B, S, dim = x.shape
     H = num_heads
     D = dim // H
-    p = {k: v.detach().cpu().double() for k, v in P.items()}
-    x = x.detach().cpu().double()
-    context = context.detach().cpu().double()
-    em = (p["modulation"] + e.detach().cpu().double()).chunk(6, dim=1)
+    p = {k: v.detach().to(device).double() for k, v in P.items()}
+    x = x.detach().to(device).double()
+    context = context.detach().to(device).double()
+    em = (p["modulation"] + e.detach().to(device).double()).chunk(6, dim=1)
 
     # self attention on norm1(x) * (1 + e1) + e0 (model.py:255-257)
     n1 = layer_norm(x, eps)
@@ -100,8 +101,12 @@ def wan_block_forward(P: dict, x, e, context, grid, src_grid, tag, freqs, num_he
     L = context.shape[1]
     qh = bf(cq).view(B, S, H, D).transpose(1, 2)
     kh = bf(ck).view(B, L, H, D).transpose(1, 2)
-    vh = cv.view(B, L, H, D).transpose(1, 2)
-    att = F.scaled_dot_product_attention(qh, kh, vh).transpose(1, 2).reshape(B, S, dim)
+    vh = cv.view(B, L, H, D).transpose(1, 2).contiguous()
+    # softmax(q k^T / sqrt(D)) v, the textbook attention (what SDPA computes), with contiguous
+    # operands and queries in chunks to bound the [S, L] score memory
+    kt = kh.transpose(-2, -1).contiguous()
+    att = torch.cat([torch.matmul(torch.softmax(torch.matmul(qh[:, :, i:i + 8192], kt) / math.sqrt(D), -1), vh)
+                     for i in range(0, S, 8192)], dim=2).transpose(1, 2).reshape(B, S, dim)
     y = linear(bf(att), p["cross_attn.o.weight"], p["cross_attn.o.bias"])
     x = x + y
 

@@ -94,7 +94,7 @@ def rope_apply(x: torch.Tensor, grid_sizes, source_grid_sizes, tag: int,
     """model.py:69-95 on x [B, S, H, D]: float64 complex product, returned as float32."""
     B, S, H, D = x.shape
     nf, nh, nw = rope_split(D)
-    out = torch.empty(B, S, H, D, dtype=torch.float32)
+    out = torch.empty(B, S, H, D, dtype=torch.float32, device=x.device)
     for b in range(B):
         pos = token_positions(S, [int(v) for v in grid_sizes[b]],
                               [int(v) for v in source_grid_sizes[b]], tag)
@@ -105,7 +105,7 @@ def rope_apply(x: torch.Tensor, grid_sizes, source_grid_sizes, tag: int,
             cols = slice(sum((nf, nh, nw)[:a]), sum((nf, nh, nw)[:a + 1]))
             rot[ok, cols] = parts[a][pos[ok, a]]
         xc = torch.view_as_complex(x[b].to(torch.float64).reshape(S, H, D // 2, 2).contiguous())
-        out[b] = torch.view_as_real(xc * rot[:, None, :]).reshape(S, H, D).float()
+        out[b] = torch.view_as_real(xc * rot.to(x.device)[:, None, :]).reshape(S, H, D).float()
     return out
 
 

@@ -20,6 +20,6 @@ def gpu():
     import torch
     if not torch.cuda.is_available():
         pytest.skip("no GPU visible")
-    from in_context_sparse_attention import _lib
+    from icsa_hip import _lib
     _lib.lib()   # fail loudly if the native library is missing
     return torch.device("cuda:0")

@@ -4,7 +4,7 @@
 The reference holds no golden vectors, known-answer tests or fixtures for this path, so
 the fixtures are produced by this repository's float64 CPU oracle (``oracle/``, itself
 pinned by tests/test_oracle.py) on seeded synthetic inputs.  Inputs are not stored:
-each fixture records the generator call (``in_context_sparse_attention.synthetic``) and
+each fixture records the generator call (``icsa_hip.synthetic``) and
 the SHA-256 of the generated bf16 bytes, so a changed generator is detected rather than
 silently compared.  Run from the repository root:
 
@@ -36,7 +36,7 @@ sys.path.insert(0, ROOT)
 sys.path.insert(0, os.path.join(ROOT, "lightning-unified-video-editor-via-in-context-sparse-attention_amd"))
 
 import oracle as O  # noqa: E402
-from in_context_sparse_attention.synthetic import make_inputs  # noqa: E402
+from icsa_hip.synthetic import make_inputs  # noqa: E402
 
 SUBSAMPLE_STRIDE = 997
 

@@ -14,7 +14,7 @@ import pytest
 import torch
 
 import oracle as O
-from in_context_sparse_attention.synthetic import make_inputs
+from icsa_hip.synthetic import make_inputs
 from parity import GAP, MAX_ABS, MEAN_ABS
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
@@ -71,7 +71,7 @@ def test_oracle_reproduces_golden(name):
 @pytest.mark.gpu
 @pytest.mark.parametrize("name", NAMES)
 def test_hip_reproduces_golden(gpu, name):
-    from in_context_sparse_attention.editing_sparse_attention import _editing_sparse_attention_hip
+    from icsa_hip.editing_sparse_attention import _editing_sparse_attention_hip
     fx = load(name)
     assert (fx["gaps"] > GAP).all(), "fixture has near-ties; decisions would not be pinned"
     q, k, v, t = regenerate(fx)

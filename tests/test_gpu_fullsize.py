@@ -1,15 +1,20 @@
-"""Parity at the benchmark sizes (65,536 and 65,520 tokens, H = 40, D = 128).
+"""Parity at the benchmark sizes (65,536 / 65,520 / 151,200 tokens, H = 40, D = 128).
 
 The whole CPU oracle is too slow at this size, so the check is split by stage, each
-part against float64 arithmetic on the same bf16 inputs:
+part against float64 arithmetic on the same bf16 inputs (the oracle's own functions,
+run in float64 on the GPU as the checker):
 
-* block sums and the compressed softmax P: the oracle's functions, run in float64;
+* block sums and the compressed softmax P;
 * every ranked decision -- source blocks, the peaked/diffuse split, the per-block exact
   lists -- must be a valid ranking of the float64 scores within GAP;
-* a sample of output rows (peaked and diffuse query blocks of several heads) against
-  float64 attention for exactly those blocks, built from the GPU's own decisions;
+* output rows of seeded-random peaked and diffuse query blocks in every head of every
+  batch entry, against float64 attention for exactly those blocks, built from the GPU's
+  own decisions;
 * size-independent properties: two runs are bit-identical, and x is exactly linear in
-  alpha_2 (x(alpha) - x(0) = alpha * out_c).
+  alpha_2 (x(alpha) - x(0) = alpha * out_c) on every token.
+
+Configuration 3 (structured K/V) is checked at every point of its sweep, flat ratio in
+{0.25, 0.5, 0.75} x SAR in {1/32, 1/16, 1/8}.
 """
 import math
 
@@ -17,20 +22,25 @@ import pytest
 import torch
 
 import oracle as O
-from in_context_sparse_attention.editing_sparse_attention import _editing_sparse_attention_hip
-from in_context_sparse_attention.synthetic import make_inputs
+from icsa_hip.editing_sparse_attention import _editing_sparse_attention_hip
+from icsa_hip.synthetic import make_inputs
 from parity import GAP, MAX_ABS, MEAN_ABS, l3_scale
 
 pytestmark = pytest.mark.gpu
 
+CFG3 = dict(H=40, real=32760, pad=8, kind="structured", seed=0)
 CASES = {
     "cfg2": dict(H=40, real=32760, pad=8, kind="random", seed=0),
-    "cfg3": dict(H=40, real=32760, pad=8, kind="structured", seed=0),
     "unaligned": dict(H=40, real=32760, pad=0, kind="random", seed=7),
     # configuration 5's attention call: 720p, 75,600 tokens per video, CFG batch B = 2
     # (NB = 2363, NKV = 1329, top_k = 83: the large-row paths of every kernel)
     "cfg5": dict(H=40, real=75600, pad=0, kind="random", seed=9, B=2),
 }
+for _flat in (0.25, 0.5, 0.75):
+    for _sar, _tag in ((1 / 32, "1/32"), (1 / 16, "1/16"), (1 / 8, "1/8")):
+        CASES[f"cfg3-flat{_flat}-sar{_tag}"] = dict(CFG3, flat_ratio=_flat, sar=_sar)
+
+SAMPLES_PER_KIND = 2          # seeded-random peaked and diffuse blocks per (batch, head)
 
 
 def _block_sums(x, NB):
@@ -41,18 +51,31 @@ def _block_sums(x, NB):
     return xp.view(B, NB, 64, H, D).sum(2).permute(0, 2, 1, 3)
 
 
+def _sample(blocks, n, gen):
+    """n seeded-random entries of each row of blocks [B, H, m] -> [B, H, min(n, m)]."""
+    B, H, m = blocks.shape
+    k = min(n, m)
+    if k == 0:
+        return blocks[..., :0]
+    pick = torch.rand(B, H, m, generator=gen, device=blocks.device).argsort(-1)[..., :k]
+    return torch.gather(blocks, -1, pick)
+
+
 @pytest.mark.parametrize("case", list(CASES))
 def test_full_size_parity(gpu, case):
+    c = dict(CASES[case])
+    sar = c.pop("sar", 0.0625)
+    flat = c.pop("flat_ratio", 0.5)
     print(f"[fullsize] {case}: generating inputs", flush=True)
-    q, k, v, t = make_inputs(**CASES[case], device=gpu)
+    q, k, v, t = make_inputs(**c, device=gpu)
     B, S, H, D = q.shape
     g = torch.Generator(device=gpu).manual_seed(11)
     alpha = (torch.rand(B, S, 1, 1, device=gpu, generator=g) - 0.5) * 0.5
-    x, views = _editing_sparse_attention_hip(q, k, v, t, alpha, keep_workspace=True)
-    x_again, _ = _editing_sparse_attention_hip(q, k, v, t, alpha)
-    x0, _ = _editing_sparse_attention_hip(q, k, v, t, 0.0)
+    x, views = _editing_sparse_attention_hip(q, k, v, t, alpha, sar, 0.125, flat, keep_workspace=True)
+    x_again, _ = _editing_sparse_attention_hip(q, k, v, t, alpha, sar, 0.125, flat)
+    x0, _ = _editing_sparse_attention_hip(q, k, v, t, 0.0, sar, 0.125, flat)
     torch.cuda.synchronize()
-    z = O.derive_sizes(B, S, H, D, t)
+    z = O.derive_sizes(B, S, H, D, t, sar, 0.125, flat)
     print(f"[fullsize] {case}: S={S} t={t} sizes={z}", flush=True)
     assert torch.equal(x, x_again), "two runs differ"
     assert torch.isfinite(x.float()).all()
@@ -62,6 +85,7 @@ def test_full_size_parity(gpu, case):
     sizes = O.block_sizes(S).to(device=gpu, dtype=torch.float64).view(1, 1, NB, 1)
     qs, ks, vs = _block_sums(q, NB), _block_sums(k, NB), _block_sums(v, NB)
     assert torch.allclose(views["q_sums"].double(), qs, rtol=1e-5, atol=1e-3)
+    assert torch.allclose(views["k_sums"].double(), ks, rtol=1e-5, atol=1e-3)
     assert torch.allclose(views["v_sums"].double(), vs, rtol=1e-5, atol=1e-3)
     P, out_c = O.compressed_attention(qs / sizes, ks / sizes, vs / sizes)
     assert torch.allclose(views["P"].double(), P, rtol=1e-4, atol=1e-7)
@@ -75,6 +99,7 @@ def test_full_size_parity(gpu, case):
     sel = views["sel"].long()
     order = views["order"].long()
     peaked, diffuse = order[..., :z.n_peaked], order[..., z.n_peaked:]
+    assert torch.equal(order.sort(-1).values, torch.arange(NB, device=gpu).expand_as(order))
     _, src_score = O.select_source_blocks(P, z.n_t, z.topK)
     assert O.check_topk_valid(src_score, sel, z.topK, GAP, ordered=True).all()
     _, _, sharp = O.split_blocks(P, z.n_t, z.k_sparsity, z.n_peaked)
@@ -88,37 +113,45 @@ def test_full_size_parity(gpu, case):
     nv = torch.gather(vh, 2, idx).masked_fill((tokmap < 0)[..., None], 0)
     nk = torch.nn.functional.pad(nk, (0, 0, 0, pad))
     nv = torch.nn.functional.pad(nv, (0, 0, 0, pad))
-    kc = nk.double().view(B, H, z.NKV, 64, D).sum(3)
     bi, hi = torch.arange(B, device=gpu).view(B, 1, 1), torch.arange(H, device=gpu).view(1, H, 1)
-    qc = qs[bi, hi, diffuse]
-    l3_scores = torch.matmul(qc, kc.transpose(-1, -2))
     l3 = views["l3"].long()
-    assert O.check_topk_valid(l3_scores / l3_scale(D), l3, z.top_k, GAP, ordered=False).all()
+    if z.n_diffuse > 0:
+        kc = nk.double().view(B, H, z.NKV, 64, D).sum(3)
+        qc = qs[bi, hi, diffuse]
+        l3_scores = torch.matmul(qc, kc.transpose(-1, -2).contiguous())
+        assert O.check_topk_valid(l3_scores / l3_scale(D), l3, z.top_k, GAP, ordered=False).all()
     print(f"[fullsize] {case}: decisions valid", flush=True)
 
-    # ---- sampled output blocks, float64 ----
+    # ---- sampled output blocks of every (batch, head), float64 ----
+    gs = torch.Generator(device=gpu).manual_seed(1234)
+    pk = _sample(peaked, SAMPLES_PER_KIND, gs)                         # [B, H, np]
+    dpos = _sample(torch.arange(z.n_diffuse, device=gpu).expand(B, H, z.n_diffuse).contiguous(),
+                   SAMPLES_PER_KIND, gs)                               # positions in `diffuse`
+    dk = torch.gather(diffuse, -1, dpos)                               # [B, H, nd]
+    qpad = torch.zeros(B, NB * 64, H, D, dtype=torch.float64, device=gpu)
+    qpad[:, :S] = q.double()
+    qblk = qpad.view(B, NB, 64, H, D).permute(0, 3, 1, 2, 4)          # [B, H, NB, 64, D]
     errs = []
-    bb = B - 1
-    for h in (0, 13, 27, H - 1):
-        for kind, blocks in (("peaked", peaked[bb, h, :2]), ("diffuse", diffuse[bb, h, :2])):
-            for blk in blocks.tolist():
-                r0, r1 = 64 * blk, min(S, 64 * blk + 64)
-                qb = torch.zeros(64, D, dtype=torch.float64, device=gpu)
-                qb[:r1 - r0] = q[bb, r0:r1, h].double()
-                if kind == "peaked":
-                    kk, vv = nk[bb, h, :z.Tkv].double(), nv[bb, h, :z.Tkv].double()
-                    s = qb @ kk.T / math.sqrt(D)
-                    ob = torch.softmax(s, -1) @ vv
-                else:
-                    pos = (diffuse[bb, h] == blk).nonzero()[0, 0].item()
-                    ob, _, _ = O.sparse_piecewise_attn(
-                        qb.cpu().view(1, 1, 64, D), nk[bb, h].cpu().view(1, 1, -1, D),
-                        nv[bb, h].cpu().view(1, 1, -1, D), 0.0625,
-                        indices=l3[bb, h, pos].cpu().view(1, 1, 1, -1))
-                    ob = ob.view(64, D).to(gpu)
-                ref = ob[:r1 - r0] + alpha[bb, r0:r1, 0].double() * out_c[bb, h, blk].view(1, D)
-                errs.append((x[bb, r0:r1, h].double() - ref).abs())
+
+    def add_err(blocks, ref):                                          # ref [B, H, n, 64, D]
+        for b in range(B):
+            for h in range(H):
+                for j, blk in enumerate(blocks[b, h].tolist()):
+                    r0, r1 = 64 * blk, min(S, 64 * blk + 64)
+                    want = ref[b, h, j, :r1 - r0] + alpha[b, r0:r1, 0].double() * out_c[b, h, blk].view(1, D)
+                    errs.append((x[b, r0:r1, h].double() - want).abs())
+
+    if pk.shape[-1] > 0:
+        qp = qblk[bi, hi, pk].reshape(B, H, -1, D)
+        s = torch.matmul(qp, nk[:, :, :z.Tkv].double().transpose(-1, -2).contiguous()) / math.sqrt(D)
+        op = torch.matmul(torch.softmax(s, -1), nv[:, :, :z.Tkv].double())
+        add_err(pk, op.view(B, H, -1, 64, D))
+    if dk.shape[-1] > 0:
+        qd = qblk[bi, hi, dk].reshape(B, H, -1, D)
+        lists = torch.gather(l3, 2, dpos[..., None].expand(-1, -1, -1, z.top_k))
+        od, _, _ = O.sparse_piecewise_attn(qd, nk.double(), nv.double(), sar, indices=lists)
+        add_err(dk, od.view(B, H, -1, 64, D))
     e = torch.cat(errs)
-    print(f"[fullsize] {case}: sampled rows max_abs={e.max().item():.3e} mean_abs={e.mean().item():.3e}",
-          flush=True)
+    print(f"[fullsize] {case}: {len(errs)} sampled blocks, max_abs={e.max().item():.3e} "
+          f"mean_abs={e.mean().item():.3e}", flush=True)
     assert e.max().item() <= MAX_ABS and e.mean().item() <= MEAN_ABS

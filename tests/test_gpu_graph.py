@@ -9,8 +9,8 @@ copied into the captured inputs must equal an eager call on that data.
 import pytest
 import torch
 
-from in_context_sparse_attention import editing_sparse_attention, sparse_piecewise_attn_1st_intervals_hip
-from in_context_sparse_attention.synthetic import make_inputs
+from icsa_hip import editing_sparse_attention, sparse_piecewise_attn_1st_intervals_hip
+from icsa_hip.synthetic import make_inputs
 
 pytestmark = pytest.mark.gpu
 
@@ -47,7 +47,7 @@ def test_graph_editing_sparse_attention(gpu):
     s = q.shape[1] - t
 
     def call():
-        return editing_sparse_attention(q, k, v, t, s, alpha_2=0.7)
+        return editing_sparse_attention(q, k, v, t, s, alpha_2=0.7, backend="hip")
 
     g, out = _capture(call)
     _check_replays(g, out, call)

@@ -5,9 +5,9 @@ import pytest
 import torch
 
 import oracle as O
-from in_context_sparse_attention import (flash_attn_func, gather_kv, pool,
-                                         sparse_piecewise_attn_1st_intervals_hip)
-from in_context_sparse_attention.hip_host import IcsaArgumentError
+from icsa_hip import (flash_attn_func, gather_kv, pool,
+                      sparse_piecewise_attn_1st_intervals_hip)
+from icsa_hip.hip_host import IcsaArgumentError
 from parity import GAP, compare_out, l3_scale
 
 pytestmark = pytest.mark.gpu

@@ -9,9 +9,9 @@ import pytest
 import torch
 
 import oracle as O
-from in_context_sparse_attention import editing_sparse_attention
-from in_context_sparse_attention.editing_sparse_attention import _editing_sparse_attention_hip
-from in_context_sparse_attention.synthetic import make_inputs
+from icsa_hip import editing_sparse_attention
+from icsa_hip.editing_sparse_attention import _editing_sparse_attention_hip
+from icsa_hip.synthetic import make_inputs
 from parity import GAP, compare_out, gpu_decisions, l3_scale
 
 pytestmark = pytest.mark.gpu
@@ -95,11 +95,11 @@ def test_flat_ratio_and_sar_sweep(gpu, flat, sar):
 def test_deterministic_and_linear_in_v(gpu):
     q, k, v, t = make_inputs(H=3, real=1536, pad=0, kind="random", seed=6)
     q, k, v = q.to(gpu), k.to(gpu), v.to(gpu)
-    x1 = editing_sparse_attention(q, k, v, t, t, alpha_2=0.5)
-    x2 = editing_sparse_attention(q, k, v, t, t, alpha_2=0.5)
+    x1 = editing_sparse_attention(q, k, v, t, t, alpha_2=0.5, backend="hip")
+    x2 = editing_sparse_attention(q, k, v, t, t, alpha_2=0.5, backend="hip")
     assert torch.equal(x1, x2), "two runs differ"
     # decisions depend on q, k only; every stage is linear in v and x2 is exact in bf16/fp32
-    x3 = editing_sparse_attention(q, k, 2 * v, t, t, alpha_2=0.5)
+    x3 = editing_sparse_attention(q, k, 2 * v, t, t, alpha_2=0.5, backend="hip")
     assert torch.equal(x3, 2 * x1), "output not exactly linear in v"
 
 

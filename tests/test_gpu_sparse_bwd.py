@@ -20,9 +20,9 @@ import torch.nn.functional as F
 
 import oracle as O
 from oracle.sparse_bwd import sparse_piecewise_attn_bwd
-from in_context_sparse_attention import (SparsePiecewiseAttn1stIntervalsFunction,
-                                         sparse_piecewise_attn_1st_intervals_bwd_hip,
-                                         sparse_piecewise_attn_1st_intervals_fwd_hip)
+from icsa_hip import (SparsePiecewiseAttn1stIntervalsFunction,
+                      sparse_piecewise_attn_1st_intervals_bwd_hip,
+                      sparse_piecewise_attn_1st_intervals_fwd_hip)
 from parity import compare_out
 
 pytestmark = pytest.mark.gpu
@@ -136,7 +136,7 @@ def test_autograd_function(gpu):
 
 
 def test_backward_bad_arguments(gpu):
-    from in_context_sparse_attention.hip_host import IcsaArgumentError
+    from icsa_hip.hip_host import IcsaArgumentError
     q = _bf16(1, 1, 128, 128).to(gpu)
     out, lse, idx = sparse_piecewise_attn_1st_intervals_fwd_hip(q, q, q, 0.5)
     with pytest.raises(IcsaArgumentError):

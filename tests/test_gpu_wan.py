@@ -16,8 +16,8 @@ import torch
 
 import oracle as O
 from oracle import wan_glue as W
-from in_context_sparse_attention import wan
-from in_context_sparse_attention.editing_sparse_attention import _editing_sparse_attention_hip
+from icsa_hip import wan
+from icsa_hip.editing_sparse_attention import _editing_sparse_attention_hip
 from parity import GAP, compare_out, gpu_decisions, l3_scale
 
 pytestmark = pytest.mark.gpu
@@ -90,7 +90,7 @@ def test_producer_tag0_and_bad_arguments(gpu):
     assert gate is None
     qo, _ = W.wan_qk(yq, yk, wq, wk, 1e-6, [(2, 3, 10)], [(1, 2, 20)], 0, freqs, H)
     _check_bf16(q, qo, "q tag 0")
-    from in_context_sparse_attention._lib import IcsaError
+    from icsa_hip._lib import IcsaError
     with pytest.raises(IcsaError):                          # grid beyond the RoPE table
         wan.wan_qk_prologue(yq.to(gpu), yk.to(gpu), wq, wk, [(2000, 1, 1)], [(1, 1, 1)], 1, freqs, H)
 

@@ -1,4 +1,4 @@
-"""GPU parity of the Wan DiT block on the HIP backend (in_context_sparse_attention.wan).
+"""GPU parity of the Wan DiT block on the HIP backend (icsa_hip.wan).
 
 * ``ln_modulate`` (icsa_wan_ln_modulate) against float64 LayerNorm / adaLN / residual.
 * ``WanAttentionBlock`` end to end against oracle.wan_block on the GPU's own self-attention
@@ -14,7 +14,7 @@ import torch
 
 from oracle import wan_block as WB
 from oracle import wan_glue as W
-from in_context_sparse_attention import wan
+from icsa_hip import wan
 from parity import gpu_decisions
 from test_wan_block_oracle import _params
 

@@ -1,4 +1,4 @@
-"""GPU parity of the Wan DiT forward on the HIP backend (in_context_sparse_attention.wan.WanModel)
+"""GPU parity of the Wan DiT forward on the HIP backend (icsa_hip.wan.WanModel)
 against oracle.wan_model, with each block's self-attention decisions captured from the GPU run.
 
 A tiny t2v model (dim 256, 2 heads, 2 blocks, FFN 512) runs one classifier-free-guidance pair
@@ -9,7 +9,7 @@ import torch
 
 from oracle import wan_glue as W
 from oracle import wan_model as WM
-from in_context_sparse_attention import wan
+from icsa_hip import wan
 from parity import gpu_decisions
 from test_wan_model_oracle import CFG, model_params
 

@@ -10,11 +10,11 @@ import pytest
 import torch
 
 import oracle as O
-from in_context_sparse_attention import _lib
-from in_context_sparse_attention.editing_sparse_attention import (
+from icsa_hip import _lib
+from icsa_hip.editing_sparse_attention import (
     SIZE_NAMES, Backend, derived_sizes, editing_sparse_attention)
-from in_context_sparse_attention.hip_host import (IcsaArgumentError, flash_attn_func,
-                                                  sparse_piecewise_attn_1st_intervals_hip)
+from icsa_hip.hip_host import (IcsaArgumentError, flash_attn_func,
+                               sparse_piecewise_attn_1st_intervals_hip)
 
 pytestmark = pytest.mark.cpu
 
@@ -133,11 +133,14 @@ def test_backend_names_and_dispatch():
     q = torch.zeros(1, 128, 1, 128, dtype=torch.bfloat16)
     with pytest.raises(NotImplementedError):
         editing_sparse_attention(q, q, q, 64, 64, backend="tilelang")
+    # the reference's default backend is 'tilelang' (editing_sparse_attention.py:67-71)
+    with pytest.raises(NotImplementedError):
+        editing_sparse_attention(q, q, q, 64, 64)
     with pytest.raises(ValueError):
         editing_sparse_attention(q, q, q, 64, 64, backend="nope")
     # CPU tensors are refused, never computed another way
     with pytest.raises(IcsaArgumentError):
-        editing_sparse_attention(q, q, q, 64, 64)
+        editing_sparse_attention(q, q, q, 64, 64, backend="hip")
 
 
 def test_host_functions_mirror_reference_asserts():
@@ -157,3 +160,19 @@ def test_product_package_never_imports_the_oracle():
             if f.endswith(".py"):
                 src = open(os.path.join(dirpath, f)).read()
                 assert not pat.search(src), f"{f} imports the oracle"
+
+
+def test_index_list_checks_reject_bad_lists():
+    from icsa_hip.hip_host import check_index_lists
+    ok = torch.tensor([[[3, 0, 5], [1, 2, 4]]])
+    check_index_lists(ok, 6, "idx")
+    with pytest.raises(IcsaArgumentError, match="distinct"):
+        check_index_lists(torch.tensor([[[3, 0, 3]]]), 6, "idx")
+    with pytest.raises(IcsaArgumentError, match="lie in"):
+        check_index_lists(torch.tensor([[[3, 0, 6]]]), 6, "idx")
+    with pytest.raises(IcsaArgumentError, match="lie in"):
+        check_index_lists(torch.tensor([[[-1, 0, 2]]]), 6, "idx")
+    check_index_lists(torch.tensor([[[-1, 0, 2]]]), 6, "idx", allow_neg=True)
+    # an injected block order must be a permutation of the blocks
+    with pytest.raises(IcsaArgumentError):
+        check_index_lists(torch.tensor([[[0, 1, 1, 3]]]), 4, "order")

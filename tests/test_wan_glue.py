@@ -130,5 +130,5 @@ def test_alpha_gate_closed_form():
 
 
 def test_package_rope_table_matches_oracle():
-    from in_context_sparse_attention import wan
+    from icsa_hip import wan
     assert torch.allclose(wan.wan_freqs(128), W.wan_freqs(128), rtol=0, atol=1e-12)
