@@ -156,6 +156,32 @@ int icsa_editing_sparse_attention_ev(
     const int32_t* inject_sel, const int32_t* inject_order, const int32_t* inject_l3,
     void* workspace, int64_t workspace_bytes, void* stream, void* const* stage_events);
 
+/* Bytes of the static device scratch of icsa_editing_sparse_attention_noalloc (256 MiB). */
+#define ICSA_NOALLOC_SCRATCH_BYTES (256LL << 20)
+
+/* icsa_editing_sparse_attention without a workspace argument and without any allocation:
+ * its scratch is a file-scope __device__ array of ICSA_NOALLOC_SCRATCH_BYTES, one per
+ * device, which the device holds until the process ends.  Same arguments (minus
+ * workspace / workspace_bytes), semantics and results as icsa_editing_sparse_attention.
+ * Calls whose workspace (icsa_editing_workspace_size) exceeds the scratch return
+ * ICSA_EUNSUPPORTED before any device work; 256 MiB covers, e.g., B = 1, S = 65,536,
+ * H <= 8 (one GPU's share of the 40 heads on 8 GPUs).  Nothing in the scratch needs to
+ * start at zero, and every call overwrites what it reads.  All calls on one device share
+ * that device's scratch: calls that overlap in time on one device (different streams or
+ * host threads without ordering) race and give undefined results.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). */
+int icsa_editing_sparse_attention_noalloc(
+    const void* q, int q_dtype, int64_t q_sb, int64_t q_ss, int64_t q_sh,
+    const void* k, int k_dtype, int64_t k_sb, int64_t k_ss, int64_t k_sh,
+    const void* v, int v_dtype, int64_t v_sb, int64_t v_ss, int64_t v_sh,
+    int B, int S, int H, int D, int t_seq_len, double sparsity, double srr, double flat_ratio,
+    const void* alpha, int alpha_dtype, int64_t a_sb, int64_t a_ss, int64_t a_sh, int64_t a_sd,
+    float alpha_scalar,
+    void* out, int out_dtype, int64_t o_sb, int64_t o_ss, int64_t o_sh,
+    const int32_t* inject_sel, const int32_t* inject_order, const int32_t* inject_l3,
+    void* stream);
+
 /* Workspace bytes of icsa_sparse_piecewise_attn. */
 int64_t icsa_sparse_piecewise_workspace_size(int B, int H, int TQ, int TKV, int D, double sparsity);
 

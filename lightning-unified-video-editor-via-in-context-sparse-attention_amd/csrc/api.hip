@@ -5,6 +5,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 
 #include "icsa_kernels.h"
@@ -419,6 +420,73 @@ int icsa_editing_sparse_attention_presummed(ICSA_EDITING_ARGS, void* const* stag
                                             const float* qsum, const float* ksum) {
   if (!qsum || !ksum) return fail(ICSA_EINVAL, "qsum / ksum are NULL");
   return editing_impl(ICSA_EDITING_PASS, stage_events, qsum, ksum);
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------------------
+// No-allocation variant of icsa_editing_sparse_attention: its workspace is this file-scope
+// device array (each device that runs the library holds its own copy until the process
+// ends).  In host code `scratch` names a host-side stand-in, never the device memory, so
+// the host only ever uses the per-device address returned by hipGetSymbolAddress.
+// ---------------------------------------------------------------------------------------
+static __device__ __align__(256) unsigned char scratch[ICSA_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_dev[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device, looked up on the first call made
+// with that device current and kept for later calls.
+int scratch_for_current_device(void** out) {
+  int dev = 0;
+  ICSA_HIP_TRY(hipGetDevice(&dev), "hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(ICSA_EUNSUPPORTED, "device %d outside the %d devices the scratch table covers", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_dev[dev] == nullptr) {
+    void* p = nullptr;
+    ICSA_HIP_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+    if (p == nullptr) return fail(ICSA_EHIP, "hipGetSymbolAddress(scratch) returned NULL");
+    g_scratch_dev[dev] = p;
+  }
+  *out = g_scratch_dev[dev];
+  return ICSA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int icsa_editing_sparse_attention_noalloc(
+    const void* q, int q_dtype, int64_t q_sb, int64_t q_ss, int64_t q_sh,
+    const void* k, int k_dtype, int64_t k_sb, int64_t k_ss, int64_t k_sh,
+    const void* v, int v_dtype, int64_t v_sb, int64_t v_ss, int64_t v_sh,
+    int B, int S, int H, int D, int t_seq_len, double sparsity, double srr, double flat_ratio,
+    const void* alpha, int alpha_dtype, int64_t a_sb, int64_t a_ss, int64_t a_sh, int64_t a_sd,
+    float alpha_scalar,
+    void* out, int out_dtype, int64_t o_sb, int64_t o_ss, int64_t o_sh,
+    const int32_t* inject_sel, const int32_t* inject_order, const int32_t* inject_l3,
+    void* stream_) {
+  // sizes first: an oversized request fails before any HIP call
+  int rc = validate_common(B, S, H, D);
+  if (rc) return rc;
+  if ((rc = check_dtype(q_dtype, "q")) || (rc = check_dtype(k_dtype, "k"))) return rc;
+  if (t_seq_len < 0 || t_seq_len > S) return fail(ICSA_EINVAL, "t_seq_len %d outside [0, S=%d]", t_seq_len, S);
+  const Sizes z = derive(S, t_seq_len, sparsity, srr, flat_ratio);
+  const int64_t need = editing_layout(B, S, H, z, t_seq_len, q_dtype, k_dtype).total;
+  if (need > (int64_t)ICSA_NOALLOC_SCRATCH_BYTES)
+    return fail(ICSA_EUNSUPPORTED,
+                "this call needs %lld bytes of scratch, more than the %lld-byte static scratch of "
+                "icsa_editing_sparse_attention_noalloc; call icsa_editing_sparse_attention with a "
+                "workspace instead", (long long)need, (long long)ICSA_NOALLOC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  if ((rc = scratch_for_current_device(&ws))) return rc;
+  void* workspace = ws;
+  const int64_t workspace_bytes = ICSA_NOALLOC_SCRATCH_BYTES;
+  return editing_impl(ICSA_EDITING_PASS, nullptr, nullptr, nullptr);
 }
 
 int icsa_wan_ln_modulate(const void* x, int x_dtype, int64_t x_sb, int64_t x_ss,

@@ -25,6 +25,9 @@ EUNSUPPORTED = -2
 EWORKSPACE = -3
 EHIP = -4
 
+# bytes of the static scratch of icsa_editing_sparse_attention_noalloc
+NOALLOC_SCRATCH_BYTES = 256 << 20
+
 # stage boundaries of icsa_editing_sparse_attention_ev
 STAGES = ["start", "pool", "compressed", "select", "sparse", "flash"]
 
@@ -37,6 +40,7 @@ WS_SLOTS = ["QSUM", "KSUM", "VSUM", "VT", "QB", "KB", "P", "OUTC", "SHARP", "SRC
 EXPORTS = [
     "icsa_editing_sizes", "icsa_editing_workspace_size", "icsa_editing_workspace_layout",
     "icsa_editing_sparse_attention", "icsa_editing_sparse_attention_ev",
+    "icsa_editing_sparse_attention_noalloc",
     "icsa_sparse_piecewise_workspace_size",
     "icsa_sparse_piecewise_attn", "icsa_flash_attn_workspace_size", "icsa_flash_attn",
     "icsa_pool", "icsa_gather_kv", "icsa_wan_qk_workspace_size", "icsa_wan_qk_prologue",
@@ -73,6 +77,15 @@ _SIGNATURES = {
         _p, _i, _l, _l, _l,
         _p, _p, _p,
         _p, _l, _p, _p]),
+    "icsa_editing_sparse_attention_noalloc": (_i, [
+        _p, _i, _l, _l, _l,
+        _p, _i, _l, _l, _l,
+        _p, _i, _l, _l, _l,
+        _i, _i, _i, _i, _i, _d, _d, _d,
+        _p, _i, _l, _l, _l, _l, _f,
+        _p, _i, _l, _l, _l,
+        _p, _p, _p,
+        _p]),
     "icsa_sparse_piecewise_workspace_size": (_l, [_i, _i, _i, _i, _i, _d]),
     "icsa_sparse_piecewise_attn": (_i, [
         _p, _l, _l, _l,

@@ -68,8 +68,13 @@ def _alpha_view(alpha_2, B, S, H, D, device):
 @torch.no_grad()
 def _editing_sparse_attention_hip(q, k, v, t_seq_len, alpha_2=1.0, SPARSITY_RATIO=0.0625,
                                   srr=0.125, flat_ratio=0.5, inject=None, keep_workspace=False,
-                                  stage_events=None, presummed=None, out_dtype=None):
+                                  stage_events=None, presummed=None, out_dtype=None, noalloc=False):
     """Runs the fused HIP path; returns ``(x, workspace_views or None)``.
+
+    ``noalloc``: use ``icsa_editing_sparse_attention_noalloc``, whose scratch is the
+    library's static device array (no workspace is allocated; the call must fit in
+    ``_lib.NOALLOC_SCRATCH_BYTES``); not combinable with ``keep_workspace``,
+    ``stage_events`` or ``presummed``.
 
     ``stage_events``: optional list of ``len(_lib.STAGES)`` recorded ``torch.cuda.Event``s
     (enable_timing=True) that the library re-records at each stage boundary on the stream.
@@ -92,7 +97,9 @@ def _editing_sparse_attention_hip(q, k, v, t_seq_len, alpha_2=1.0, SPARSITY_RATI
                                                dtype_code(k), ctypes.cast(offs, ctypes.c_void_p))
     if ws_bytes < 0:
         raise _lib.IcsaError("icsa_editing_workspace_layout", int(ws_bytes))
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
+    _require(not noalloc or (not keep_workspace and stage_events is None and presummed is None),
+             "noalloc cannot be combined with keep_workspace, stage_events or presummed")
+    ws = None if noalloc else torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
     out = torch.empty(B, S, H, D, dtype=out_dtype or q.dtype, device=q.device)
     sums_args = []
     if presummed is not None:
@@ -126,6 +133,10 @@ def _editing_sparse_attention_hip(q, k, v, t_seq_len, alpha_2=1.0, SPARSITY_RATI
     if presummed is not None:
         fn = L.icsa_editing_sparse_attention_presummed
         ev_args = (ev_args or [None]) + [ptr(presummed[0]), ptr(presummed[1])]
+    ws_args = [ptr(ws), ws_bytes]
+    if noalloc:
+        fn = L.icsa_editing_sparse_attention_noalloc
+        ws_args = []
     rc = fn(
         ptr(q), dtype_code(q), q.stride(0), q.stride(1), q.stride(2),
         ptr(k), dtype_code(k), k.stride(0), k.stride(1), k.stride(2),
@@ -134,8 +145,8 @@ def _editing_sparse_attention_hip(q, k, v, t_seq_len, alpha_2=1.0, SPARSITY_RATI
         ptr(a), a_dt, a_st[0], a_st[1], a_st[2], a_st[3], float(a_scalar),
         ptr(out), dtype_code(out), out.stride(0), out.stride(1), out.stride(2),
         ptr(inj.get("sel")), ptr(inj.get("order")), ptr(inj.get("l3")),
-        ptr(ws), ws_bytes, stream_ptr(q.device), *ev_args)
-    _lib.check("icsa_editing_sparse_attention", rc)
+        *ws_args, stream_ptr(q.device), *ev_args)
+    _lib.check(fn.__name__, rc)
     if not keep_workspace:
         return out, None
     return out, workspace_views(ws, list(offs), sizes, B, H, D)

@@ -176,3 +176,12 @@ def test_index_list_checks_reject_bad_lists():
     # an injected block order must be a permutation of the blocks
     with pytest.raises(IcsaArgumentError):
         check_index_lists(torch.tensor([[[0, 1, 1, 3]]]), 4, "order")
+
+
+def test_noalloc_entry_rejects_oversized_calls_before_device_work():
+    # configuration 2 with all 40 heads needs more than the static scratch; the call fails
+    # on its size before any HIP call (the pointers are never read)
+    args = _editing_args(S=65536, t=32768)
+    args[17] = 40                          # H
+    rc, msg = _status("icsa_editing_sparse_attention_noalloc", *args[:-3], None)
+    assert rc == _lib.EUNSUPPORTED and "static scratch" in msg
