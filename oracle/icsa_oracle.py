@@ -268,10 +268,14 @@ def split_blocks(P: torch.Tensor, n_t: int, k_sparsity: int, n_peaked: int):
 # ---------------------------------------------------------------------------------------
 
 def dense_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
-                    chunk: int = 4096) -> torch.Tensor:
+                    chunk: Optional[int] = None) -> torch.Tensor:
     """Textbook non-causal softmax attention ``[..., T, D]`` (flash_attn_func at
-    editing_sparse_attention.py:211-215), chunked over queries to bound memory."""
+    editing_sparse_attention.py:211-215), chunked over queries to bound memory (default:
+    at most 2^27 score elements per chunk, and at most 4096 queries)."""
     D = q.shape[-1]
+    if chunk is None:
+        lead = q[..., 0, 0].numel()
+        chunk = max(16, min(4096, (1 << 27) // max(1, lead * k.shape[-2])))
     outs = []
     kt = k.transpose(-2, -1).contiguous()
     for s0 in range(0, q.shape[-2], chunk):

@@ -94,3 +94,67 @@ def test_block_matches_oracle(gpu):
     print(f"[block] max_abs={mx:.3e} mean_abs={mn:.3e} |x|max={ref.abs().max().item():.2f}", flush=True)
     assert torch.isfinite(out).all()
     assert mx <= 3e-2 and mn <= 3e-3, (mx, mn)
+
+
+def _params_full(dim, ffn, seed, device):
+    """Block parameters at full width: xavier-uniform Linear weights (the reference's
+    init_weights, model.py:395-408), small random biases, modulation ~ N(0, 1/dim)."""
+    g = torch.Generator(device=device).manual_seed(seed)
+
+    def xavier(o, i):
+        a = math.sqrt(6.0 / (i + o))
+        return ((torch.rand(o, i, generator=g, device=device) * 2 - 1) * a).to(torch.bfloat16)
+
+    def rn(*shape, s):
+        return (torch.randn(*shape, generator=g, device=device) * s).to(torch.bfloat16)
+
+    P = {"modulation": (torch.randn(1, 6, dim, generator=g, device=device) / math.sqrt(dim))}
+    for pre in ("self_attn", "cross_attn"):
+        for n in ("q", "k", "v", "o"):
+            P[f"{pre}.{n}.weight"] = xavier(dim, dim)
+            P[f"{pre}.{n}.bias"] = rn(dim, s=0.01)
+        P[f"{pre}.alpha_1.weight"] = xavier(1, dim)
+        P[f"{pre}.alpha_2.weight"] = torch.zeros(1, dim, device=device)
+        P[f"{pre}.norm_q.weight"] = 1 + rn(dim, s=0.1).float()
+        P[f"{pre}.norm_k.weight"] = 1 + rn(dim, s=0.1).float()
+    P["norm3.weight"] = 1 + rn(dim, s=0.1).float()
+    P["norm3.bias"] = rn(dim, s=0.1).float()
+    P["ffn.0.weight"] = xavier(ffn, dim)
+    P["ffn.0.bias"] = rn(ffn, s=0.01)
+    P["ffn.2.weight"] = xavier(dim, ffn)
+    P["ffn.2.bias"] = rn(dim, s=0.01)
+    return P
+
+
+def test_block_full_width_cfg4(gpu):
+    """Configuration 4 at its real width: dim 5120, 40 heads, FFN 13,824, 21x30x52 target and
+    source grids (65,520 tokens, t % 64 != 0), 512 text tokens.  The oracle runs the whole
+    block in float64 on the GPU on the block's own self-attention decisions."""
+    dim, ffn, H = 5120, 13824, 40
+    grid = (21, 30, 52)
+    S = 2 * math.prod(grid)
+    print(f"[block-cfg4] dim={dim} ffn={ffn} H={H} S={S}", flush=True)
+    P = _params_full(dim, ffn, 5, gpu)
+    blk = wan.WanAttentionBlock("t2v_cross_attn", dim, ffn, H, cross_attn_norm=True)
+    blk.load_state_dict({k: v.float().cpu() for k, v in P.items()}, strict=True)
+    blk = blk.to(gpu).to(torch.bfloat16)
+    g = torch.Generator(device=gpu).manual_seed(12)
+    x = torch.randn(1, S, dim, generator=g, device=gpu)
+    e = torch.randn(1, 6, dim, generator=g, device=gpu) * 0.1
+    ctx = torch.randn(1, 512, dim, generator=g, device=gpu).to(torch.bfloat16)
+    freqs = W.wan_freqs(128)
+    blk.self_attn.capture = {}
+    out = blk(x.clone(), e, torch.tensor([S]), [grid], freqs, ctx, None, [grid], 1)
+    torch.cuda.synchronize()
+    dec = gpu_decisions(blk.self_attn.capture["views"])
+    blk.self_attn.capture = None
+    Pb = {k: v.detach() for k, v in blk.state_dict().items()}          # the bf16 values used
+    print("[block-cfg4] HIP block done; float64 oracle on the GPU", flush=True)
+    ref, info = WB.wan_block_forward(Pb, x, e, ctx, grid, grid, 1, freqs, H, decisions=dec, device=gpu)
+    torch.cuda.synchronize()
+    d = (out.double() - ref).abs()
+    mx, mn = d.max().item(), d.mean().item()
+    print(f"[block-cfg4] max_abs={mx:.3e} mean_abs={mn:.3e} |x|max={ref.abs().max().item():.2f}",
+          flush=True)
+    assert torch.isfinite(out).all()
+    assert mx <= 3e-2 and mn <= 3e-3, (mx, mn)
