@@ -182,7 +182,8 @@ int icsa_editing_sparse_attention_noalloc(
     const int32_t* inject_sel, const int32_t* inject_order, const int32_t* inject_l3,
     void* stream);
 
-/* Workspace bytes of icsa_sparse_piecewise_attn. */
+/* Workspace bytes of icsa_sparse_piecewise_attn and icsa_sparse_piecewise_attn_fwd (ragged
+ * TQ / TKV are sized in whole 64-token blocks). */
 int64_t icsa_sparse_piecewise_workspace_size(int B, int H, int TQ, int TKV, int D, double sparsity);
 
 /* Sparse piecewise attention (first-order intervals) on q [B, H, TQ, D], k/v [B, H, TKV, D]
@@ -200,10 +201,16 @@ int icsa_sparse_piecewise_attn(
     void* out, int64_t o_sb, int64_t o_sh, int64_t o_st,
     void* workspace, int64_t workspace_bytes, void* stream);
 
-/* The same forward (workspace: icsa_sparse_piecewise_workspace_size) with the state its
- * backward needs: idx_out [B*H, TQ/64, top_k] (required) and lse_out [B*H, TQ] f32
- * (required), the log-sum-exp in log2 units as the Triton forward stores it: the final
- * running max of the log2-scaled scores plus log2(l + g_l). */
+/* The Triton host's forward (workspace: icsa_sparse_piecewise_workspace_size) with the state
+ * its backward needs.  Contract of triton_host.py:11-30 / triton_kernels.py:489-539: TQ and
+ * TKV need not be multiples of 64 (rows past them read as zeros in the block sums); the
+ * top_k = max(1, int(sparsity * (TKV / 64))) exact blocks (integer division: the floor) are
+ * chosen among cdiv(TKV, 64) candidates; keys at or past TKV take no part in the exact
+ * attention (triton_kernels.py:185); the interval covers all cdiv(TKV, 64) blocks.  For
+ * TQ, TKV multiples of 64 the result equals icsa_sparse_piecewise_attn's.
+ * idx_out [B*H, cdiv(TQ, 64), top_k] (required) and lse_out [B*H, TQ] f32 (required), the
+ * log-sum-exp in log2 units as the Triton forward stores it: the final running max of the
+ * log2-scaled scores plus log2(l + g_l). */
 int icsa_sparse_piecewise_attn_fwd(
     const void* q, int64_t q_sb, int64_t q_sh, int64_t q_st,
     const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st,
@@ -220,7 +227,8 @@ int64_t icsa_sparse_piecewise_attn_bwd_workspace_size(int B, int H, int TQ, int 
  * [B, H, TKV, D] bf16 (strides sb, sh, st), lse [B*H, TQ] and idx [B*H, TQ/64, top_k]
  * from the forward (distinct block indices per row; entries outside [0, TKV/64) are
  * skipped).  dq / dk / dv are written (not accumulated) as bf16 or f32 (dtype codes).
- * Deterministic: every gradient is a fixed-order sum, no atomics. */
+ * Deterministic: every gradient is a fixed-order sum, no atomics.  TQ and TKV must be
+ * multiples of 64 (ICSA_EINVAL otherwise; the forward also takes ragged lengths). */
 int icsa_sparse_piecewise_attn_bwd(
     const void* dout, int64_t do_sb, int64_t do_sh, int64_t do_st,
     const void* q, int64_t q_sb, int64_t q_sh, int64_t q_st,

@@ -382,6 +382,7 @@ int editing_impl(ICSA_EDITING_ARGS, void* const* stage_events, const float* qsum
     s.kc = np.kc; s.vct = np.vct;
     s.out_c = cp.out_c; s.nb_q = z.NB;
     s.alpha = av; s.out = ov; s.scale_log2 = scale_log2; s.lse = nullptr;
+    s.mask_tail = 0;                   // zero-padded new KV attended with logit 0 (TileLang)
     ICSA_HIP_TRY(launch_sparse(s, stream), "sparse attention");
   }
   ICSA_HIP_TRY(mark(ICSA_STAGE_SPARSE), "event");
@@ -601,9 +602,12 @@ namespace {
 struct SpLayout {
   int64_t qsum, ksum, vsum, vt, kc32, kc, vct, idx, scores, total;
 };
+// Sizes for TQ / TKV rounded up to whole blocks (the Triton host's ragged lengths); the
+// index buffer holds max(1, int(sparsity * NKV)) entries per query block, which is at
+// least the Triton host's floor top_k.
 SpLayout sparse_layout(int B, int H, int TQ, int TKV, double sparsity) {
   const int64_t BH = (int64_t)B * H;
-  const int NQ = TQ / ICSA_BLOCK, NKV = TKV / ICSA_BLOCK;
+  const int NQ = ceil_div(TQ, ICSA_BLOCK), NKV = ceil_div(TKV, ICSA_BLOCK);
   const int NKVp = ceil_div(NKV, 64) * 64;
   const int top_k = std::max(1, (int)(sparsity * (double)NKV));
   SpLayout L;
@@ -611,7 +615,7 @@ SpLayout sparse_layout(int B, int H, int TQ, int TKV, double sparsity) {
   L.qsum = o; o += align256(BH * NQ * ICSA_D * 4);
   L.ksum = o; o += align256(BH * NKV * ICSA_D * 4);
   L.vsum = o; o += align256(BH * NKV * ICSA_D * 4);
-  L.vt = o; o += align256(BH * ICSA_D * (int64_t)TKV * 2);
+  L.vt = o; o += align256(BH * ICSA_D * (int64_t)NKV * ICSA_BLOCK * 2);
   L.kc32 = o; o += align256(BH * NKV * ICSA_D * 4);
   L.kc = o; o += align256(BH * NKVp * ICSA_D * 2);
   L.vct = o; o += align256(BH * ICSA_D * NKVp * 2);
@@ -626,10 +630,15 @@ extern "C" {
 
 int64_t icsa_sparse_piecewise_workspace_size(int B, int H, int TQ, int TKV, int D, double sparsity) {
   if (B <= 0 || H <= 0 || TQ <= 0 || TKV <= 0 || D != ICSA_D) return ICSA_EINVAL;
-  if (TQ % ICSA_BLOCK || TKV % ICSA_BLOCK || !(sparsity > 0.0)) return ICSA_EINVAL;
+  if (!(sparsity > 0.0)) return ICSA_EINVAL;
   return sparse_layout(B, H, TQ, TKV, sparsity).total;
 }
 
+// triton == 0: the TileLang host (tilelang_host.py:229-274): TQ, TKV multiples of 64,
+//   top_k = max(1, int(sparsity * NKV)).
+// triton == 1: the Triton host (triton_host.py:11-30 -> triton_kernels.py:489-539): ragged
+//   TQ / TKV, NKV = cdiv(TKV, 64) candidate blocks, top_k = max(1, int(sparsity *
+//   (TKV // 64))), keys >= TKV masked out of the exact part.
 static int sparse_piecewise_impl(
     const void* q, int64_t q_sb, int64_t q_sh, int64_t q_st,
     const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st,
@@ -637,20 +646,20 @@ static int sparse_piecewise_impl(
     int B, int H, int TQ, int TKV, int D, double sparsity,
     const int32_t* inject_idx, int32_t* idx_out,
     void* out, int64_t o_sb, int64_t o_sh, int64_t o_st, float* lse_out,
-    void* workspace, int64_t workspace_bytes, void* stream_) {
+    void* workspace, int64_t workspace_bytes, void* stream_, int triton) {
   int rc = validate_common(B, TQ, H, D);
   if (rc) return rc;
   if (TKV <= 0) return fail(ICSA_EINVAL, "TKV must be positive");
-  if (TQ % ICSA_BLOCK || TKV % ICSA_BLOCK)
+  if (!triton && (TQ % ICSA_BLOCK || TKV % ICSA_BLOCK))
     return fail(ICSA_EINVAL, "TQ/TKV must be divisible by the block size 64 (got %d, %d)", TQ, TKV);
   if (!q || !k || !v || !out || !workspace) return fail(ICSA_EINVAL, "null q/k/v/out/workspace pointer");
   if (!row_ok(q, ICSA_BF16, q_sb, q_sh, q_st) || !row_ok(k, ICSA_BF16, k_sb, k_sh, k_st) ||
       !row_ok(v, ICSA_BF16, v_sb, v_sh, v_st) || !row_ok(out, ICSA_BF16, o_sb, o_sh, o_st))
     return fail(ICSA_EINVAL, "q/k/v/out rows must be 16-byte aligned (pointer and strides)");
   if (!(sparsity > 0.0)) return fail(ICSA_EINVAL, "sparsity must be > 0");
-  const int NQ = TQ / ICSA_BLOCK, NKV = TKV / ICSA_BLOCK;
+  const int NQ = ceil_div(TQ, ICSA_BLOCK), NKV = ceil_div(TKV, ICSA_BLOCK);
   const int NKVp = ceil_div(NKV, 64) * 64;
-  const int top_k = std::max(1, (int)(sparsity * (double)NKV));
+  const int top_k = std::max(1, (int)(sparsity * (double)(triton ? TKV / ICSA_BLOCK : NKV)));
   if (NKV > 2048 || top_k > 512 || top_k > NKV)
     return fail(ICSA_EUNSUPPORTED, "NKV=%d / top_k=%d exceed limits (2048 / 512)", NKV, top_k);
   const SpLayout L = sparse_layout(B, H, TQ, TKV, sparsity);
@@ -673,8 +682,9 @@ static int sparse_piecewise_impl(
   pk.x[2] = TokTensor{v, v_sb, v_st, v_sh, ICSA_BF16};
   pk.sums[1] = reinterpret_cast<float*>(ws + L.ksum);
   pk.sums[2] = reinterpret_cast<float*>(ws + L.vsum);
+  const int64_t TKVp = (int64_t)NKV * ICSA_BLOCK;   // V^T columns (zeros past TKV)
   pk.vt = reinterpret_cast<bf16*>(ws + L.vt);
-  pk.vt_sb = (int64_t)H * ICSA_D * TKV; pk.vt_sh = (int64_t)ICSA_D * TKV; pk.vt_sd = TKV;
+  pk.vt_sb = (int64_t)H * ICSA_D * TKVp; pk.vt_sh = (int64_t)ICSA_D * TKVp; pk.vt_sd = TKVp;
   pk.vt_src = 2;
   pk.B = B; pk.S = TKV; pk.H = H; pk.NB = NKV;
   ICSA_HIP_TRY(launch_pool(pk, stream), "pool k/v");
@@ -716,6 +726,7 @@ static int sparse_piecewise_impl(
   s.out = OutView{out, o_sb, o_st, o_sh, ICSA_BF16};
   s.scale_log2 = kLog2e / std::sqrt((float)ICSA_D);
   s.lse = lse_out;
+  s.mask_tail = triton;
   ICSA_HIP_TRY(launch_sparse(s, stream), "sparse attention");
   return ICSA_OK;
 }
@@ -730,7 +741,7 @@ int icsa_sparse_piecewise_attn(
     void* workspace, int64_t workspace_bytes, void* stream) {
   return sparse_piecewise_impl(q, q_sb, q_sh, q_st, k, k_sb, k_sh, k_st, v, v_sb, v_sh, v_st, B, H,
                                TQ, TKV, D, sparsity, inject_idx, idx_out, out, o_sb, o_sh, o_st,
-                               nullptr, workspace, workspace_bytes, stream);
+                               nullptr, workspace, workspace_bytes, stream, 0);
 }
 
 int icsa_sparse_piecewise_attn_fwd(
@@ -744,7 +755,7 @@ int icsa_sparse_piecewise_attn_fwd(
   if (!idx_out || !lse_out) return fail(ICSA_EINVAL, "idx_out and lse_out are required (saved for the backward)");
   return sparse_piecewise_impl(q, q_sb, q_sh, q_st, k, k_sb, k_sh, k_st, v, v_sb, v_sh, v_st, B, H,
                                TQ, TKV, D, sparsity, inject_idx, idx_out, out, o_sb, o_sh, o_st,
-                               lse_out, workspace, workspace_bytes, stream);
+                               lse_out, workspace, workspace_bytes, stream, 1);
 }
 
 // ---------------------------------------------------------------------------------------

@@ -139,6 +139,9 @@ struct SparseParams {
   const bf16* k; int64_t k_sb, k_st, k_sh;      // keys: b, token, h strides
   const bf16* vt; int64_t vt_sb, vt_sh, vt_sd;  // [B, H, D, Tp]
   int B, H, Sq, Sk;                  // Sk: tokens available in k/vt (rows >= Sk read as 0)
+  int mask_tail;                     // 1: exact-part keys >= Sk take no part (the Triton
+                                     // host, triton_kernels.py:185); 0: they are zero keys
+                                     // attended with logit 0 (TileLang's zero padding)
   const int* qblocks; int qb_offset, qb_stride; int n_qblk;
   const int* kvmap; int kvmap_identity;         // [BH, NKV] source block of new-KV block
   const int* idx;                    // [BH, n_qblk, top_k] ascending

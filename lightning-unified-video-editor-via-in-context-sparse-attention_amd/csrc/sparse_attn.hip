@@ -24,7 +24,9 @@
 // (k, vt) buffers -- target blocks and the selected source blocks of the original
 // sequence -- or is an all-zero block (kvmap -1 / an out-of-range caller index, the
 // reference's TKV zero padding, attended with logit 0).  KC / VC^T are the bf16 block sums
-// of the new KV.
+// of the new KV.  With mask_tail (the Triton host's ragged TKV) the keys of an exact block
+// at or past Sk get no weight instead (triton_kernels.py:185); the interval part is the
+// same in both modes.
 //
 // Workgroup = 2 waves = one query block (wave w: rows 32 w .. 32 w + 31); four workgroups
 // share a CU.  One K buffer and one V^T buffer per workgroup, filled by direct
@@ -291,6 +293,13 @@ icsa_sparse_kernel(SparseParams p) {
     qk();
     ATT_BARRIER();                       // K buffer free
     const int kv_next = issue_k(t + 1);    // T > T1: always a next K tile
+    if (p.mask_tail && kv_pending < ATT_BN) {  // keys past Sk take no part (Triton host)
+#pragma unroll
+      for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          if (32 * sub + acc_row(i, lane) >= kv_pending) s[sub][i] = -INFINITY;
+    }
     float mx = -INFINITY;
 #pragma unroll
     for (int sub = 0; sub < 2; ++sub)

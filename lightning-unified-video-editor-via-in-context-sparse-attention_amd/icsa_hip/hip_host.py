@@ -1,10 +1,13 @@
 """HIP host functions with the reference's kernel-host signatures.
 
 * :func:`sparse_piecewise_attn_1st_intervals_hip` mirrors
-  ``sparse_piecewise_attn_1st_intervals_tilelang`` (tilelang_host.py:229-274) and the Triton
-  ``sparse_piecewise_attn_1st_intervals`` (triton_host.py:11-30): same arguments, shapes,
-  dtypes, return value and ownership.  Argument checks raise :class:`IcsaArgumentError`, an
-  ``AssertionError`` (what the reference's asserts raise) that is also a ``ValueError``.
+  ``sparse_piecewise_attn_1st_intervals_tilelang`` (tilelang_host.py:229-274): same
+  arguments, shapes, dtypes, return value and ownership, and the TileLang asserts.
+  Argument checks raise :class:`IcsaArgumentError`, an ``AssertionError`` (what the
+  reference's asserts raise) that is also a ``ValueError``.
+* :func:`sparse_piecewise_attn_1st_intervals` mirrors the Triton host of the same name
+  (triton_host.py:11-30), whose contract differs: ragged TQ / TKV, floor top_k over
+  TKV // 64, keys past TKV masked out of the exact part (triton_kernels.py:185, 489-539).
 * :func:`flash_attn_func` mirrors the call made at editing_sparse_attention.py:211-215
   (flash-attn's ``flash_attn_func(q, k, v)``, dense non-causal, default scale).
 * :func:`pool` and :func:`gather_kv` expose stage 1 and the new-KV gather.
@@ -131,12 +134,9 @@ def sparse_piecewise_attn_1st_intervals_hip(q: torch.Tensor, k: torch.Tensor, v:
     return (out, idx_out) if return_indices else out
 
 
-# the Triton host's name (triton_host.py:11) for callers that import it directly
-sparse_piecewise_attn_1st_intervals = sparse_piecewise_attn_1st_intervals_hip
-
-
-def _check_sparse_args(q, k, v, block_size):
-    """The TileLang host's argument checks (tilelang_host.py:251-259)."""
+def _check_sparse_args(q, k, v, block_size, aligned=True):
+    """The TileLang host's argument checks (tilelang_host.py:251-259); ``aligned=False``
+    drops the multiple-of-64 lengths the Triton host does not need."""
     _require(q.dtype == k.dtype == v.dtype == torch.bfloat16, "q, k, v must be bfloat16")
     _require(q.is_cuda and k.is_cuda and v.is_cuda, "q, k, v must be on the GPU")
     _require(block_size == 64, "Only block_size=64 supported.")
@@ -146,24 +146,36 @@ def _check_sparse_args(q, k, v, block_size):
     _require(q.shape[3] == k.shape[3], "Kdim must match between q and k")
     _require(k.shape[2] == v.shape[2], "TKV must match between k and v")
     _require(v.shape[3] == q.shape[3], "This entrypoint assumes Vdim == D (so VBlocks==1).")
-    _require(q.shape[2] % BLOCK_M == 0 and k.shape[2] % BLOCK_M == 0, "TQ/TKV must be divisible by BT")
+    _require(q.shape[2] > 0 and k.shape[2] > 0, "TQ and TKV must be positive")
+    if aligned:
+        _require(q.shape[2] % BLOCK_M == 0 and k.shape[2] % BLOCK_M == 0, "TQ/TKV must be divisible by BT")
+
+
+def triton_top_k(sparsity: float, TKV: int) -> int:
+    """Exact blocks per query block of the Triton host: max(1, int(sparsity * (TKV // 64)))
+    (triton_kernels.py:501), over cdiv(TKV, 64) candidate blocks."""
+    return max(1, int(sparsity * (TKV // BLOCK_M)))
 
 
 @torch.no_grad()
 def sparse_piecewise_attn_1st_intervals_fwd_hip(q, k, v, sparsity: float = 0.1, block_size: int = 64,
                                                 indices: torch.Tensor = None):
     """The forward of SparsePiecewiseAttn1stIntervalsFunction (triton_kernels.py:489-539)
-    with the state its backward needs.  Returns ``(out, lse, indices)``: out bf16
+    with the state its backward needs, under the Triton host's contract: TQ and TKV need
+    not be multiples of 64 (rows past them read as zeros in the block sums), the
+    ``top_k = max(1, int(sparsity * (TKV // 64)))`` exact blocks are chosen among
+    ``cdiv(TKV, 64)`` candidates, and keys at or past TKV take no part in the exact
+    attention (triton_kernels.py:185).  Returns ``(out, lse, indices)``: out bf16
     [B, H, TQ, D]; lse f32 [B, H, TQ] in log2 units (the final running max of the
     log2-scaled scores plus log2 of the combined denominator); indices int32
-    [B, H, TQ/64, top_k] (``indices`` given: used instead of the kernel's own top-k)."""
-    _check_sparse_args(q, k, v, block_size)
+    [B, H, cdiv(TQ, 64), top_k] (``indices`` given: used instead of the kernel's own top-k)."""
+    _check_sparse_args(q, k, v, block_size, aligned=False)
     B, H, TQ, D = q.shape
     TKV = k.shape[2]
     q, k, v = inner_contiguous(q), inner_contiguous(k), inner_contiguous(v)
     L = _lib.lib()
-    NQ, NKV = TQ // BLOCK_M, TKV // BLOCK_M
-    top_k = max(1, int(sparsity * NKV))
+    NQ, NKV = (TQ + BLOCK_M - 1) // BLOCK_M, (TKV + BLOCK_M - 1) // BLOCK_M
+    top_k = triton_top_k(sparsity, TKV)
     out = torch.empty(B, H, TQ, D, dtype=torch.bfloat16, device=q.device)
     lse = torch.empty(B, H, TQ, dtype=torch.float32, device=q.device)
     idx = torch.empty(B, H, NQ, top_k, dtype=torch.int32, device=q.device)
@@ -189,6 +201,18 @@ def sparse_piecewise_attn_1st_intervals_fwd_hip(q, k, v, sparsity: float = 0.1, 
 
 
 @torch.no_grad()
+def sparse_piecewise_attn_1st_intervals(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                                        sparsity: float = 0.1, block_size: int = 64) -> torch.Tensor:
+    """The Triton host (triton_host.py:11-30) on MI355X: ``SparsePiecewiseAttn1stIntervals
+    Function.apply`` under ``no_grad``.  q [B, H, TQ, D], k / v [B, H, TKV, D] bfloat16 with
+    any TQ and TKV (the reference's Triton branch passes the unpadded new KV,
+    editing_sparse_attention.py:203-207); floor top_k over TKV // 64, keys past TKV masked
+    out of the exact part.  Returns a new bf16 [B, H, TQ, D] owned by the caller."""
+    out, _, _ = sparse_piecewise_attn_1st_intervals_fwd_hip(q, k, v, sparsity, block_size)
+    return out
+
+
+@torch.no_grad()
 def sparse_piecewise_attn_1st_intervals_bwd_hip(do, q, k, v, out, lse, indices, grad_dtype=None,
                                                 check_indices=True):
     """Gradients ``(dq, dk, dv)`` of the sparse piecewise attention, as
@@ -198,7 +222,8 @@ def sparse_piecewise_attn_1st_intervals_bwd_hip(do, q, k, v, out, lse, indices, 
     or float32.  ``indices`` must hold distinct blocks in ``[0, TKV/64)`` per query block
     (the forward's top-k always does; the reference's atomics would count a repeated entry
     twice in every gradient, this build's key-major dk / dv pass once), which
-    ``check_indices`` verifies on the host (one device sync)."""
+    ``check_indices`` verifies on the host (one device sync).  TQ and TKV must be multiples
+    of 64 here (the forward also takes ragged lengths)."""
     _check_sparse_args(q, k, v, 64)
     B, H, TQ, D = q.shape
     TKV = k.shape[2]

@@ -54,20 +54,25 @@ def bf_compressed(qc, kc, vc):
     return P, out
 
 
-def bf_sparse_piecewise(q, k, v, sparsity, order_exact=None):
+def bf_sparse_piecewise(q, k, v, sparsity, order_exact=None, triton=False):
     """One (b,h) of the sparse kernel, scalar loops.  q [TQ,D], k/v [TKV,D].
 
     For every query row: online softmax over the selected blocks key by key, then the
     interval chunks (64 compressed blocks each) with the non-rescaled g_acc/g_l.
     ``order_exact`` optionally fixes the per-block index lists (any order).
+    ``triton``: the Triton host's contract (triton_kernels.py:489-539): TQ and TKV need not
+    be multiples of 64; a block's sums run over its real rows, the exact loop visits only
+    keys below TKV (triton_kernels.py:185), and top_k = max(1, int(sparsity * (TKV // 64))).
     """
     TQ, D = q.shape
     TKV = k.shape[0]
-    NQ, NKV = TQ // BLOCK_M, TKV // BLOCK_M
-    QC = np.array([q[n * 64:(n + 1) * 64].sum(0) for n in range(NQ)])
-    KC = np.array([k[n * 64:(n + 1) * 64].sum(0) for n in range(NKV)])
-    VC = np.array([v[n * 64:(n + 1) * 64].sum(0) for n in range(NKV)])
-    top_k = max(1, int(sparsity * NKV))
+    if not triton:
+        assert TQ % BLOCK_M == 0 and TKV % BLOCK_M == 0
+    NQ, NKV = -(-TQ // BLOCK_M), -(-TKV // BLOCK_M)
+    QC = np.array([q[n * 64:min(TQ, (n + 1) * 64)].sum(0) for n in range(NQ)])
+    KC = np.array([k[n * 64:min(TKV, (n + 1) * 64)].sum(0) for n in range(NKV)])
+    VC = np.array([v[n * 64:min(TKV, (n + 1) * 64)].sum(0) for n in range(NKV)])
+    top_k = max(1, int(sparsity * (TKV // BLOCK_M if triton else NKV)))
     scale = 1.0 / math.sqrt(D)
     out = np.zeros((TQ, D))
     idx_all = []
@@ -78,10 +83,10 @@ def bf_sparse_piecewise(q, k, v, sparsity, order_exact=None):
             scores = [float(np.dot(QC[n], KC[j])) for j in range(NKV)]
             sel = _rank(scores)[:top_k]
         idx_all.append(sorted(sel))
-        for r in range(n * 64, (n + 1) * 64):
+        for r in range(n * 64, min(TQ, (n + 1) * 64)):
             m, l, acc = -math.inf, 0.0, np.zeros(D)
             for blk in sel:
-                for key in range(blk * 64, (blk + 1) * 64):
+                for key in range(blk * 64, min(TKV, (blk + 1) * 64)):
                     s = float(np.dot(q[r], k[key])) * scale
                     m_new = max(m, s)
                     a = math.exp(m - m_new) if m != -math.inf else 0.0

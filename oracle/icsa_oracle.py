@@ -286,8 +286,17 @@ def dense_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
 
 def sparse_piecewise_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                           sparsity: float = 0.1, indices: Optional[torch.Tensor] = None,
-                          dtype=torch.float64, qchunk: int = 64, return_lse: bool = False):
+                          dtype=torch.float64, qchunk: int = 64, return_lse: bool = False,
+                          mode: str = "tilelang"):
     """Sparse piecewise attention with the first-order interval approximation.
+
+    ``mode="triton"`` follows the Triton host instead (triton_host.py:11-30 ->
+    SparsePiecewiseAttn1stIntervalsFunction.forward, triton_kernels.py:489-539, kernel
+    :122-263), which takes ragged TQ / TKV: block sums over the real rows (zero fill,
+    :89-119), ``NKV = cdiv(TKV, 64)`` candidate blocks, ``top_k = max(1, int(sparsity *
+    (TKV // 64)))`` (floor, :501), keys at positions >= TKV masked out of the exact part
+    (:185), and the interval over all NKV blocks with /64 and weight 64 like TileLang
+    (:206-242).  For TQ and TKV multiples of 64 both modes give the same result.
 
     Semantics of ``sparse_piecewise_attn_1st_intervals_tilelang`` (tilelang_host.py:229-274
     -> :121-206 -> tilelang_kernels.py:681-997).  ``q [B,H,TQ,D]``, ``k``/``v [B,H,TKV,D]``
@@ -310,18 +319,24 @@ def sparse_piecewise_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     backward (triton_kernels.py:249-252): ``m + log2(l + g_l)`` in log2 units (the final
     running max of the log2-scaled scores; ``-inf`` where the denominator is 0).
     """
-    B, H, TQ, D = q.shape
-    TKV = k.shape[2]
-    assert TQ % BLOCK_M == 0 and TKV % BLOCK_M == 0
-    NQ, NKV = TQ // BLOCK_M, TKV // BLOCK_M
+    assert mode in ("tilelang", "triton")
+    B, H, TQ_real, D = q.shape
+    TKV_real = k.shape[2]
+    if mode == "tilelang":
+        assert TQ_real % BLOCK_M == 0 and TKV_real % BLOCK_M == 0
     dev = q.device              # every intermediate follows the inputs' device
+    TQ, TKV = ceil_div(TQ_real, BLOCK_M) * BLOCK_M, ceil_div(TKV_real, BLOCK_M) * BLOCK_M
+    NQ, NKV = TQ // BLOCK_M, TKV // BLOCK_M
     scale = 1.0 / math.sqrt(D)
-    qd, kd, vd = q.to(dtype), k.to(dtype), v.to(dtype)
+    # rows past the real lengths are zeros (the Triton kernels' boundary fill)
+    qd = F.pad(q.to(dtype), (0, 0, 0, TQ - TQ_real))
+    kd = F.pad(k.to(dtype), (0, 0, 0, TKV - TKV_real))
+    vd = F.pad(v.to(dtype), (0, 0, 0, TKV - TKV_real))
     QC = qd.view(B, H, NQ, BLOCK_M, D).sum(3)
     KC = kd.view(B, H, NKV, BLOCK_M, D).sum(3)
     VC = vd.view(B, H, NKV, BLOCK_M, D).sum(3)
     scores = torch.matmul(QC, KC.transpose(-2, -1).contiguous())
-    top_k = max(1, int(sparsity * NKV))
+    top_k = max(1, int(sparsity * (NKV if mode == "tilelang" else TKV_real // BLOCK_M)))
     if indices is None:
         indices = ranked_topk(scores, top_k)
     indices = torch.sort(indices.long().to(dev), dim=-1).values
@@ -340,6 +355,10 @@ def sparse_piecewise_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         kx = kb[bi, hi, idx].reshape(B, H, n1 - n0, top_k * BLOCK_M, D)
         vx = vb[bi, hi, idx].reshape(B, H, n1 - n0, top_k * BLOCK_M, D)
         s_ex = torch.matmul(qb, kx.transpose(-2, -1).contiguous()) * scale
+        if TKV_real < TKV:      # Triton: keys past TKV do not take part (triton_kernels.py:185)
+            kpos = (idx[..., None] * BLOCK_M + torch.arange(BLOCK_M, device=dev)).reshape(
+                B, H, n1 - n0, 1, top_k * BLOCK_M)
+            s_ex = s_ex.masked_fill(kpos >= TKV_real, -math.inf)
         m = s_ex.max(-1).values
         p = torch.exp(s_ex - m[..., None])
         l = p.sum(-1)
@@ -367,6 +386,7 @@ def sparse_piecewise_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         out[:, :, n0 * BLOCK_M:n1 * BLOCK_M] = o.reshape(B, H, (n1 - n0) * BLOCK_M, D)
         lse[:, :, n0 * BLOCK_M:n1 * BLOCK_M] = ((m + torch.log(den)) / math.log(2.0)).reshape(
             B, H, (n1 - n0) * BLOCK_M)
+    out, lse = out[:, :, :TQ_real], lse[:, :, :TQ_real]
     if return_lse:
         return out, indices, scores, lse
     return out, indices, scores

@@ -84,7 +84,11 @@ def test_size_queries_reject_bad_arguments():
     assert rc == _lib.EINVAL
     rc, _ = _status("icsa_editing_sizes", 1, 1024, 1, 128, 512, 0.0625, 0.125, 0.5, None)
     assert rc == _lib.EINVAL
-    assert _lib.lib().icsa_sparse_piecewise_workspace_size(1, 1, 100, 128, 128, 0.1) < 0
+    assert _lib.lib().icsa_sparse_piecewise_workspace_size(1, 1, 128, 128, 96, 0.1) < 0
+    assert _lib.lib().icsa_sparse_piecewise_workspace_size(1, 1, 128, 128, 128, 0.0) < 0
+    # ragged lengths (the Triton host) are sized in whole blocks
+    assert (_lib.lib().icsa_sparse_piecewise_workspace_size(1, 1, 100, 4645, 128, 0.1)
+            == _lib.lib().icsa_sparse_piecewise_workspace_size(1, 1, 128, 4672, 128, 0.1))
     assert _lib.lib().icsa_flash_attn_workspace_size(1, 128, 1, 96) < 0
 
 

@@ -388,3 +388,69 @@ def test_topk_checker_rejects_planted_mistakes():
     # within tolerance a near-tie may go either way
     near = torch.tensor([[1.0, 1.0 + 1e-9, 0.0]], dtype=DT)
     assert O.check_topk_valid(near, torch.tensor([[0]]), 1, 1e-6, ordered=True).all()
+
+
+# ----------------------------------------------------------------------------------------
+# the Triton host's contract (triton_host.py:11-30; triton_kernels.py:89-119, 185, 489-539):
+# ragged TQ / TKV, floor top_k, keys past TKV masked out of the exact part
+# ----------------------------------------------------------------------------------------
+
+def test_sparse_triton_mode_equals_tilelang_for_aligned_lengths():
+    q = _randn(1, 2, 128, 16, seed=30)
+    k = _randn(1, 2, 64 * 9, 16, seed=31)
+    v = _randn(1, 2, 64 * 9, 16, seed=32)
+    a = O.sparse_piecewise_attn(q, k, v, 0.25)
+    b = O.sparse_piecewise_attn(q, k, v, 0.25, mode="triton")
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+
+
+def test_sparse_triton_mode_all_selected_is_attention_over_the_real_keys():
+    # TKV = 4 * 64 + 37: five candidate blocks, the last partial; sparsity 1.25 gives
+    # top_k = int(1.25 * (TKV // 64)) = 5, so every block is exact and the interval is empty:
+    # the result is textbook attention over the 293 real keys (ragged TQ as well)
+    q = _randn(1, 2, 133, 16, seed=33)
+    k = _randn(1, 2, 293, 16, seed=34)
+    v = _randn(1, 2, 293, 16, seed=35)
+    out, idx, _ = O.sparse_piecewise_attn(q, k, v, 1.25, mode="triton")
+    assert idx.shape[-1] == 5 and out.shape == (1, 2, 133, 16)
+    assert torch.allclose(out, _sdpa(q, k, v), rtol=0, atol=1e-13)
+
+
+@pytest.mark.parametrize("tq,tkv,sp,seed", [(133, 293, 0.5, 36), (64, 64 * 70 + 11, 0.05, 37),
+                                            (100, 64 * 129 + 63, 0.02, 38)])
+def test_sparse_triton_mode_matches_bruteforce_loops(tq, tkv, sp, seed):
+    D = 8
+    q = _randn(1, 1, tq, D, seed=seed)
+    k = _randn(1, 1, tkv, D, seed=seed + 100)
+    v = _randn(1, 1, tkv, D, seed=seed + 200)
+    out, idx, _ = O.sparse_piecewise_attn(q, k, v, sparsity=sp, mode="triton")
+    ob, ib = BF.bf_sparse_piecewise(q[0, 0].numpy(), k[0, 0].numpy(), v[0, 0].numpy(), sp, triton=True)
+    assert idx[0, 0].tolist() == ib
+    assert np.allclose(out[0, 0].numpy(), ob, rtol=0, atol=1e-12)
+
+
+def test_sparse_triton_mode_masks_the_tail_instead_of_attending_zero_keys():
+    # a planted mistake -- the tail keys of the partial block attended with logit 0, as
+    # TileLang's zero padding does -- differs clearly from the Triton contract
+    q = _randn(1, 1, 64, 8, seed=39) * 0.3
+    k = _randn(1, 1, 64 * 3 + 5, 8, seed=40) * 0.3
+    v = _randn(1, 1, 64 * 3 + 5, 8, seed=41) + 2.0
+    idx = torch.tensor([0, 1, 2, 3]).view(1, 1, 1, 4)
+    tri, _, _ = O.sparse_piecewise_attn(q, k, v, 1.34, indices=idx, mode="triton")
+    kp = torch.cat([k, torch.zeros(1, 1, 59, 8, dtype=DT)], 2)
+    vp = torch.cat([v, torch.zeros(1, 1, 59, 8, dtype=DT)], 2)
+    pad_logit0, _, _ = O.sparse_piecewise_attn(q, kp, vp, 1.0, indices=idx)
+    assert torch.allclose(tri, _sdpa(q, k, v), atol=1e-13)
+    assert (tri - pad_logit0).abs().max() > 0.3      # 59 zero keys of 256 pull the mean of v ~ 2 down
+
+
+def test_sparse_triton_top_k_floor_at_configuration_4():
+    # the DiT block's unpadded new KV: Tkv = 36,856 (Appendix A): Triton 35 exact blocks,
+    # TileLang (zero-padded to 36,864) 36
+    q = _randn(1, 1, 64, 4, seed=42)
+    k = _randn(1, 1, 36856, 4, seed=43)
+    _, idx_tri, sc = O.sparse_piecewise_attn(q, k, k, 0.0625, mode="triton")
+    assert idx_tri.shape[-1] == 35 and sc.shape[-1] == 576
+    kp = torch.cat([k, torch.zeros(1, 1, 8, 4, dtype=DT)], 2)
+    _, idx_tl, _ = O.sparse_piecewise_attn(q, kp, kp, 0.0625)
+    assert idx_tl.shape[-1] == 36
