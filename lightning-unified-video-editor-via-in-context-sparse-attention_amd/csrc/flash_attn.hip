@@ -26,9 +26,11 @@
 // once, the tile start is the scalar base of a buffer resource whose range covers only key
 // rows below Sk, and every LDS offset is hoisted out of the loop.
 //
-// Softmax state: probabilities are taken relative to a reference max m_ref that is raised
-// only when a row max exceeds it by more than FA_RESCALE_LOG2 (so p <= 2^8); the O / l
-// rescale then runs on a few tiles per row.  Exact in real arithmetic.
+// Softmax state: probabilities are taken relative to a reference max m_ref, computed first
+// and checked afterwards: only when a lane's partial sum of the tile exceeds 2^64 (or is NaN,
+// as against the initial m_ref = -inf) is the row max of the tile taken, the reference
+// raised, O / l rescaled and the tile recomputed.  In the common case no per-tile max
+// reduction precedes the exponentials.  Exact in real arithmetic.
 #include "attn_tile.h"
 #include "icsa_kernels.h"
 
@@ -42,7 +44,10 @@
 #define FA_JUNK_OFF (FA_TILE_BYTES + 4 * FA_MAX_SEL)         // landing area of disabled DMA
 #define FA_LOOP_BYTES (FA_JUNK_OFF + 4096)
 #define FA_LDS_BYTES (FA_LOOP_BYTES > FA_STAGE_BYTES ? FA_LOOP_BYTES : FA_STAGE_BYTES)
-#define FA_RESCALE_LOG2 8.0f
+// A lane's 32 probabilities of a tile sum to at most 2^64 relative to the row's reference
+// max before the reference is raised: O and l then stay below 2^64 * keys * |v|, far inside
+// the fp32 range, and bf16(p) keeps its relative precision at any magnitude.
+#define FA_PSUM_MAX 18446744073709551616.0f
 #ifndef FA_PF
 #define FA_PF 3             // operand prefetch depth (MFMA steps)
 #endif
@@ -190,8 +195,9 @@ icsa_flash_kernel(FlashParams p) {
   auto dma_seg = [&](int i) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(dma_rs, (lds_ptr)(dma_dst + 1024 * i), 16, dofs[i], 0, 0, 0);
   };
-  // SOFT(k): mask, row max, lazy rescale, P(k); the wave's DMA segments go out one at a time
-  // between the exponentials
+  // SOFT(k): mask, P(k) against the reference max, and -- only when some probability of the
+  // tile left the allowed range -- a rescale to the tile's row max and a second pass.  The
+  // wave's DMA segments go out one at a time between the exponentials of the first pass.
   auto soft = [&](int k) {
     const int mask_from = k < p.n_tgt_tiles ? p.t_limit - k * ATT_BN : ATT_BN;
     if (mask_from < ATT_BN) {
@@ -200,23 +206,6 @@ icsa_flash_kernel(FlashParams p) {
 #pragma unroll
         for (int i = 0; i < 16; ++i)
           if (32 * sub + acc_row(i, lane) >= mask_from) s[sub][i] = -INFINITY;
-    }
-    float mx = -INFINITY;
-#pragma unroll
-    for (int sub = 0; sub < 2; ++sub)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[sub][i]);
-    mx = xhalf_max(mx) * c;
-    const bool need = mx > m_ref + FA_RESCALE_LOG2;
-    if (__ballot(need) != 0ull) {
-      const float mn = need ? mx : m_ref;
-      const float a = __builtin_amdgcn_exp2f(m_ref - mn);
-#pragma unroll
-      for (int ds = 0; ds < 4; ++ds)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) o[ds][i] *= a;
-      l_run *= a;
-      m_ref = mn;
     }
     float rs = 0.f;
 #pragma unroll
@@ -232,6 +221,34 @@ icsa_flash_kernel(FlashParams p) {
         rs += e;
         pf[2 * sb + (i >> 3)][i & 7] = (bf16)e;
       }
+    // The partial sum exceeds FA_PSUM_MAX (or is NaN: the first tile, against m_ref = -inf)
+    // only when a score rose far above the reference: then raise the reference of every row
+    // whose tile max exceeds it, rescale O and l, and recompute the tile's probabilities.
+    if (__ballot(!(rs <= FA_PSUM_MAX)) != 0ull) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[sub][i]);
+      mx = xhalf_max(mx) * c;
+      const float mn = mx > m_ref ? mx : m_ref;
+      const float a = __builtin_amdgcn_exp2f(m_ref - mn);
+#pragma unroll
+      for (int ds = 0; ds < 4; ++ds)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o[ds][i] *= a;
+      l_run *= a;
+      m_ref = mn;
+      rs = 0.f;
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const float e = __builtin_amdgcn_exp2f(fmaf(s[sb][i], c, -m_ref));
+          rs += e;
+          pf[2 * sb + (i >> 3)][i & 7] = (bf16)e;
+        }
+    }
     l_run += rs;
   };
 
