@@ -83,11 +83,11 @@ enum icsa_ws_slot {
   ICSA_WS_KVMAP,      /* i32 [B*H, NKV]     new-KV block -> source block (-1 zero)   */
   ICSA_WS_KC32,       /* f32 [B*H, NKV, D]  new-KV block sums of k                   */
   ICSA_WS_KC,         /* bf16 [B*H, NKVp, D]                                        */
-  ICSA_WS_VCT,        /* bf16 [B*H, D, NKVp] new-KV block sums of v, transposed      */
+  ICSA_WS_VCT,        /* bf16 [B*H, D, NKVp] new-KV block sums of v, transposed (t % 64 == 0 only) */
   ICSA_WS_L3,         /* i32 [B*H, n_diffuse, top_k] per-block exact lists (ascending) */
   ICSA_WS_KN,         /* bf16 [B*H, Tp, D]  materialised new K (t % 64 != 0 only)    */
   ICSA_WS_VN,         /* bf16 [B*H, Tp, D]  materialised new V (t % 64 != 0 only)    */
-  ICSA_WS_VTN,        /* bf16 [B*H, D, Tp]  its transpose (t % 64 != 0 only)         */
+  ICSA_WS_VC,         /* bf16 [B*H, NKVp, D] new-KV block sums of v (t % 64 != 0 only) */
   ICSA_WS_NKSUM,      /* f32 [B*H, NKV, D]  (t % 64 != 0 only)                       */
   ICSA_WS_NVSUM,      /* f32 [B*H, NKV, D]  (t % 64 != 0 only)                       */
   ICSA_WS_COLP,       /* f32 [B*H, ceil(n_t/64), n_s] source-column mass per target strip */

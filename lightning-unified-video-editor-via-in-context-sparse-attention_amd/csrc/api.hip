@@ -101,12 +101,12 @@ Layout editing_layout(int B, int S, int H, const Sizes& z, int t, int q_dtype, i
   sz[ICSA_WS_KVMAP] = BH * z.NKV * 4;
   sz[ICSA_WS_KC32] = BH * z.NKV * D * 4;
   sz[ICSA_WS_KC] = BH * z.NKVp * D * 2;
-  sz[ICSA_WS_VCT] = BH * D * z.NKVp * 2;
+  sz[ICSA_WS_VCT] = unaligned ? 0 : BH * D * z.NKVp * 2;
   sz[ICSA_WS_L3] = BH * std::max(z.n_diffuse, 1) * z.top_k * 4;
   const int64_t Tp = z.TKV_pad;
   sz[ICSA_WS_KN] = unaligned ? BH * Tp * D * 2 : 0;
   sz[ICSA_WS_VN] = unaligned ? BH * Tp * D * 2 : 0;
-  sz[ICSA_WS_VTN] = unaligned ? BH * D * Tp * 2 : 0;
+  sz[ICSA_WS_VC] = unaligned ? BH * z.NKVp * D * 2 : 0;
   sz[ICSA_WS_NKSUM] = unaligned ? BH * z.NKV * D * 4 : 0;
   sz[ICSA_WS_NVSUM] = unaligned ? BH * z.NKV * D * 4 : 0;
   sz[ICSA_WS_COLP] = BH * ceil_div(z.n_t, ICSA_BLOCK) * std::max(z.n_s, 1) * 4;
@@ -306,18 +306,19 @@ int editing_impl(ICSA_EDITING_ARGS, void* const* stage_events, const float* qsum
   NewKvSumsParams np;
   np.kc32 = reinterpret_cast<float*>(WS(ICSA_WS_KC32));
   np.kc = reinterpret_cast<bf16*>(WS(ICSA_WS_KC));
-  np.vct = reinterpret_cast<bf16*>(WS(ICSA_WS_VCT));
+  np.vct = unaligned ? nullptr : reinterpret_cast<bf16*>(WS(ICSA_WS_VCT));
+  np.vc = unaligned ? reinterpret_cast<bf16*>(WS(ICSA_WS_VC)) : nullptr;
   np.BH = BH; np.NKV = z.NKV; np.NKVp = z.NKVp;
   const bf16* sk_k;            // key source of the sparse kernel
   int64_t sk_sb, sk_st, sk_sh;
-  const bf16* sk_vt;
-  int64_t sk_vsb, sk_vsh, sk_vsd;
+  const bf16* sk_v;             // values of the sparse kernel: V^T (aligned) or rows
+  int64_t sk_vs0, sk_vs1, sk_vs2;
   int sk_Sk;
   if (!unaligned) {
     np.ksum = ksum; np.vsum = pp.sums[2];
     np.kvmap = sp.kvmap; np.map_identity = 0; np.Nsrc = z.NB;
     sk_k = kb; sk_sb = kb_sb; sk_st = kb_ss; sk_sh = kb_sh;
-    sk_vt = pp.vt; sk_vsb = pp.vt_sb; sk_vsh = pp.vt_sh; sk_vsd = pp.vt_sd;
+    sk_v = pp.vt; sk_vs0 = pp.vt_sb; sk_vs1 = pp.vt_sh; sk_vs2 = pp.vt_sd;
     sk_Sk = S;
   } else {
     const int64_t Tp = z.TKV_pad;
@@ -336,15 +337,12 @@ int editing_impl(ICSA_EDITING_ARGS, void* const* stage_events, const float* qsum
     pn.x[2] = TokTensor{gp.vn, (int64_t)H * Tp * ICSA_D, ICSA_D, Tp * ICSA_D, ICSA_BF16};
     pn.sums[1] = reinterpret_cast<float*>(WS(ICSA_WS_NKSUM));
     pn.sums[2] = reinterpret_cast<float*>(WS(ICSA_WS_NVSUM));
-    pn.vt = reinterpret_cast<bf16*>(WS(ICSA_WS_VTN));
-    pn.vt_sb = (int64_t)H * ICSA_D * Tp; pn.vt_sh = ICSA_D * Tp; pn.vt_sd = Tp;
-    pn.vt_src = 2;
     pn.B = B; pn.S = (int)Tp; pn.H = H; pn.NB = z.NKV;
     ICSA_HIP_TRY(launch_pool(pn, stream), "pool new KV");
     np.ksum = pn.sums[1]; np.vsum = pn.sums[2];
     np.kvmap = nullptr; np.map_identity = 1; np.Nsrc = z.NKV;
     sk_k = gp.kn; sk_sb = (int64_t)H * Tp * ICSA_D; sk_st = ICSA_D; sk_sh = Tp * ICSA_D;
-    sk_vt = pn.vt; sk_vsb = pn.vt_sb; sk_vsh = pn.vt_sh; sk_vsd = pn.vt_sd;
+    sk_v = gp.vn; sk_vs0 = (int64_t)H * Tp * ICSA_D; sk_vs1 = ICSA_D; sk_vs2 = Tp * ICSA_D;   // rows
     sk_Sk = (int)Tp;
   }
   if (z.n_diffuse > 0) ICSA_HIP_TRY(launch_newkv_sums(np, stream), "new-KV sums");
@@ -374,12 +372,19 @@ int editing_impl(ICSA_EDITING_ARGS, void* const* stage_events, const float* qsum
     SparseParams s;
     s.q = qb; s.q_sb = qb_sb; s.q_ss = qb_ss; s.q_sh = qb_sh;
     s.k = sk_k; s.k_sb = sk_sb; s.k_st = sk_st; s.k_sh = sk_sh;
-    s.vt = sk_vt; s.vt_sb = sk_vsb; s.vt_sh = sk_vsh; s.vt_sd = sk_vsd;
+    s.v_rows = unaligned ? 1 : 0;
+    if (unaligned) {
+      s.v = sk_v; s.v_sb = sk_vs0; s.v_st = sk_vs1; s.v_sh = sk_vs2;
+      s.vt = nullptr; s.vt_sb = s.vt_sh = s.vt_sd = 0;
+    } else {
+      s.vt = sk_v; s.vt_sb = sk_vs0; s.vt_sh = sk_vs1; s.vt_sd = sk_vs2;
+      s.v = nullptr; s.v_sb = s.v_st = s.v_sh = 0;
+    }
     s.B = B; s.H = H; s.Sq = S; s.Sk = sk_Sk;
     s.qblocks = order; s.qb_offset = z.n_peaked; s.qb_stride = z.NB; s.n_qblk = z.n_diffuse;
     s.kvmap = sp.kvmap; s.kvmap_identity = unaligned ? 1 : 0;
     s.idx = l3; s.top_k = z.top_k; s.NKV = z.NKV; s.NKVp = z.NKVp;
-    s.kc = np.kc; s.vct = np.vct;
+    s.kc = np.kc; s.vct = np.vct; s.vc = np.vc;
     s.out_c = cp.out_c; s.nb_q = z.NB;
     s.alpha = av; s.out = ov; s.scale_log2 = scale_log2; s.lse = nullptr;
     s.mask_tail = 0;                   // zero-padded new KV attended with logit 0 (TileLang)
@@ -600,7 +605,7 @@ int icsa_wan_qk_prologue(
 
 namespace {
 struct SpLayout {
-  int64_t qsum, ksum, vsum, vt, kc32, kc, vct, idx, scores, total;
+  int64_t qsum, ksum, vsum, kc32, kc, vc, idx, scores, total;
 };
 // Sizes for TQ / TKV rounded up to whole blocks (the Triton host's ragged lengths); the
 // index buffer holds max(1, int(sparsity * NKV)) entries per query block, which is at
@@ -615,10 +620,9 @@ SpLayout sparse_layout(int B, int H, int TQ, int TKV, double sparsity) {
   L.qsum = o; o += align256(BH * NQ * ICSA_D * 4);
   L.ksum = o; o += align256(BH * NKV * ICSA_D * 4);
   L.vsum = o; o += align256(BH * NKV * ICSA_D * 4);
-  L.vt = o; o += align256(BH * ICSA_D * (int64_t)NKV * ICSA_BLOCK * 2);
   L.kc32 = o; o += align256(BH * NKV * ICSA_D * 4);
   L.kc = o; o += align256(BH * NKVp * ICSA_D * 2);
-  L.vct = o; o += align256(BH * ICSA_D * NKVp * 2);
+  L.vc = o; o += align256(BH * NKVp * ICSA_D * 2);
   L.idx = o; o += align256(BH * NQ * top_k * 4);
   L.scores = o; o += align256(BH * NQ * (int64_t)NKV * 4);
   L.total = o;
@@ -682,10 +686,6 @@ static int sparse_piecewise_impl(
   pk.x[2] = TokTensor{v, v_sb, v_st, v_sh, ICSA_BF16};
   pk.sums[1] = reinterpret_cast<float*>(ws + L.ksum);
   pk.sums[2] = reinterpret_cast<float*>(ws + L.vsum);
-  const int64_t TKVp = (int64_t)NKV * ICSA_BLOCK;   // V^T columns (zeros past TKV)
-  pk.vt = reinterpret_cast<bf16*>(ws + L.vt);
-  pk.vt_sb = (int64_t)H * ICSA_D * TKVp; pk.vt_sh = (int64_t)ICSA_D * TKVp; pk.vt_sd = TKVp;
-  pk.vt_src = 2;
   pk.B = B; pk.S = TKV; pk.H = H; pk.NB = NKV;
   ICSA_HIP_TRY(launch_pool(pk, stream), "pool k/v");
 
@@ -693,7 +693,8 @@ static int sparse_piecewise_impl(
   np.ksum = pk.sums[1]; np.vsum = pk.sums[2]; np.kvmap = nullptr; np.map_identity = 1;
   np.kc32 = reinterpret_cast<float*>(ws + L.kc32);
   np.kc = reinterpret_cast<bf16*>(ws + L.kc);
-  np.vct = reinterpret_cast<bf16*>(ws + L.vct);
+  np.vct = nullptr;
+  np.vc = reinterpret_cast<bf16*>(ws + L.vc);
   np.BH = BH; np.Nsrc = NKV; np.NKV = NKV; np.NKVp = NKVp;
   ICSA_HIP_TRY(launch_newkv_sums(np, stream), "block sums");
 
@@ -715,12 +716,14 @@ static int sparse_piecewise_impl(
   SparseParams s;
   s.q = reinterpret_cast<const bf16*>(q); s.q_sb = q_sb; s.q_ss = q_st; s.q_sh = q_sh;
   s.k = reinterpret_cast<const bf16*>(k); s.k_sb = k_sb; s.k_st = k_st; s.k_sh = k_sh;
-  s.vt = pk.vt; s.vt_sb = pk.vt_sb; s.vt_sh = pk.vt_sh; s.vt_sd = pk.vt_sd;
+  s.v_rows = 1;                      // v read in place, row tiles
+  s.v = reinterpret_cast<const bf16*>(v); s.v_sb = v_sb; s.v_st = v_st; s.v_sh = v_sh;
+  s.vt = nullptr; s.vt_sb = s.vt_sh = s.vt_sd = 0;
   s.B = B; s.H = H; s.Sq = TQ; s.Sk = TKV;
   s.qblocks = nullptr; s.qb_offset = 0; s.qb_stride = 0; s.n_qblk = NQ;
   s.kvmap = nullptr; s.kvmap_identity = 1;
   s.idx = idx; s.top_k = top_k; s.NKV = NKV; s.NKVp = NKVp;
-  s.kc = np.kc; s.vct = np.vct;
+  s.kc = np.kc; s.vct = nullptr; s.vc = np.vc;
   s.out_c = nullptr; s.nb_q = NQ;
   s.alpha = make_alpha(nullptr, ICSA_F32, 0, 0, 0, 0, 0.f);
   s.out = OutView{out, o_sb, o_st, o_sh, ICSA_BF16};

@@ -166,6 +166,80 @@ __device__ __forceinline__ void pv_tile(floatx16 o[4], const bf16* vs, const bf1
   }
 }
 
+// ---------------------------------------------------------------------------------------
+// Row tiles: 64 rows x 128 dims bf16, row-major as in the caller's tensors, for operands
+// that are needed transposed (V in PV, and K / Q / dO in the backward).  16-byte chunk c of
+// row r sits at slot c ^ swz(r).
+//  * rt_swz (backward tiles, also read untransposed): a bijection of r % 16, so 16-byte
+//    operand reads of 16 consecutive rows (one chunk) hit 16 distinct slots;
+//  * rv_swz (the forward kernels' V tiles, only ever read transposed): r % 4 alone, so rows
+//    8 apart share a slot pattern.
+// Both move rows 4 a + x (x = 0..3) to different slot quadrants, so a transposing read
+// (4 rows x 4 chunk positions x 2 halves per half-wave) touches 32 distinct 8-byte bank
+// pairs.
+// ---------------------------------------------------------------------------------------
+__device__ __forceinline__ int rt_swz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
+__device__ __forceinline__ int rv_swz(int r) { return (r & 3) << 2; }
+template <bool RV>
+__device__ __forceinline__ int tile_swz(int r) { return RV ? rv_swz(r) : rt_swz(r); }
+__device__ __forceinline__ int rt_off(int row, int chunk) {        // in bf16 elements
+  return row * ICSA_D + ((chunk ^ rt_swz(row)) << 3);
+}
+
+typedef short rt_v4s __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) rt_v4s* rt_lds_v4s;
+
+// Transposed MFMA operands straight from a row tile (ds_read_b64_tr_b16).  Within each
+// group of 16 lanes, lane j of the transposing read receives element j % 4 of the 4-element
+// vectors read by lanes j / 4 + 4 e (e = 0..3).  For the A operand of
+// O^T[d][key] += X^T[d][row] P[row][key] (X a 64 x 128 row tile, lane l = 16 g + s holding
+// A[d = 32 ds + l % 32][k = 8 (l / 32) + e]) with the row order of the score accumulators
+// (k -> row 16 m + 8 (e / 4) + 4 (l / 32) + e % 4), lane 16 g + s reads the 4 dims
+// 32 ds + 16 (g % 2) + 4 (s % 4) .. + 3 of row 16 m + 4 (g / 2) + s / 4 (+ 8 for e >= 4).
+// tro[ds]: those byte offsets (rows 0..7, e < 4) for m = 0; step m adds 16 rows.  The
+// rows 8 further on (e >= 4) are derived, not stored: rv_swz(r + 8) = rv_swz(r), a constant
+// 8-row offset; rt_swz(r + 8) = rt_swz(r) ^ 2 for r < 8, slot bit 1 (byte bit 5) flipped.
+template <bool RV>
+__device__ __forceinline__ void rt_tr_offsets(int tro[4], int lane) {
+  const int g = lane >> 4, s = lane & 15;
+  const int row = 4 * (g >> 1) + (s >> 2);
+#pragma unroll
+  for (int ds = 0; ds < 4; ++ds) {
+    const int col = 32 * ds + 16 * (g & 1) + 4 * (s & 3);
+    tro[ds] = row * (ICSA_D * 2) + (((col >> 3) ^ tile_swz<RV>(row)) << 4) + (col & 7) * 2;
+  }
+}
+template <bool RV>
+__device__ __forceinline__ int rt_tr_hi(int off) { return (RV ? off : (off ^ 32)) + 8 * ICSA_D * 2; }
+
+// The transposed A operand of PV step t = 4 m + ds (two transposing reads).
+template <bool RV>
+__device__ __forceinline__ bf16x8 rt_tr_operand(const unsigned char* tile, const int tro[4], int t) {
+  const int m = t >> 2, ds = t & 3;
+  const rt_v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((rt_lds_v4s)(tile + tro[ds] + m * 16 * ICSA_D * 2));
+  const rt_v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (rt_lds_v4s)(tile + rt_tr_hi<RV>(tro[ds]) + m * 16 * ICSA_D * 2));
+  const short __attribute__((ext_vector_type(8))) a8 = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  return __builtin_bit_cast(bf16x8, a8);
+}
+
+// o[4 d-subtiles] += X^T P for a row tile X (bytes at `tile`); p[m]: bf16 B operand of
+// 16-row step m, straight from the score accumulators.  Each operand is read PF steps ahead.
+template <int PF, bool RV>
+__device__ __forceinline__ void pv_tile_tr(floatx16 o[4], const unsigned char* tile, const int tro[4],
+                                           const bf16x8 p[4]) {
+  bf16x8 a[16];
+#pragma unroll
+  for (int t = 0; t < PF; ++t) a[t] = rt_tr_operand<RV>(tile, tro, t);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int t = 0; t < 16; ++t) {
+    if (t + PF < 16) a[t + PF] = rt_tr_operand<RV>(tile, tro, t + PF);
+    o[t & 3] = mfma32x32x16(a[t], p[t >> 2], o[t & 3]);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
 // bf16 B operand of PV step m from the score registers (keys of sub-tile m/2, half m%2).
 __device__ __forceinline__ void pack_p(bf16x8 p[4], const floatx16 s[2]) {
 #pragma unroll

@@ -414,7 +414,8 @@ __global__ void __launch_bounds__(128) icsa_newkv_sums_kernel(NewKvSumsParams p)
   }
   if (j < p.NKV) p.kc32[((int64_t)bh * p.NKV + j) * ICSA_D + d] = ks;
   p.kc[((int64_t)bh * p.NKVp + j) * ICSA_D + d] = f2bf(ks);
-  p.vct[((int64_t)bh * ICSA_D + d) * p.NKVp + (j & ~15) + kv_slot(j & 15)] = f2bf(vs);
+  if (p.vct) p.vct[((int64_t)bh * ICSA_D + d) * p.NKVp + (j & ~15) + kv_slot(j & 15)] = f2bf(vs);
+  if (p.vc) p.vc[((int64_t)bh * p.NKVp + j) * ICSA_D + d] = f2bf(vs);
 }
 
 hipError_t launch_newkv_sums(const NewKvSumsParams& p, hipStream_t stream) {

@@ -52,7 +52,8 @@ struct NewKvSumsParams {
   int map_identity;     // 1: kvmap ignored, block j -> j
   float* kc32;          // [BH, NKV, D]   fp32 sums of new-KV blocks
   bf16* kc;             // [BH, NKVp, D]  bf16 sums (rows >= NKV zero)
-  bf16* vct;            // [BH, D, NKVp]  bf16 sums transposed, kv_slot() order
+  bf16* vct;            // [BH, D, NKVp]  bf16 sums of v transposed, kv_slot() order (nullptr: none)
+  bf16* vc;             // [BH, NKVp, D]  bf16 sums of v, row-major (nullptr: none)
   int BH, Nsrc, NKV, NKVp;
 };
 hipError_t launch_newkv_sums(const NewKvSumsParams& p, hipStream_t stream);
@@ -137,8 +138,13 @@ hipError_t launch_ln_mod(const LnModParams& p, hipStream_t stream);
 struct SparseParams {
   const bf16* q; int64_t q_sb, q_ss, q_sh;      // [B, Sq, H, D]
   const bf16* k; int64_t k_sb, k_st, k_sh;      // keys: b, token, h strides
-  const bf16* vt; int64_t vt_sb, vt_sh, vt_sd;  // [B, H, D, Tp]
-  int B, H, Sq, Sk;                  // Sk: tokens available in k/vt (rows >= Sk read as 0)
+  // values in one of two layouts (the kernel is instantiated for each):
+  int v_rows;                        // 1: row-major v (b, token, h strides, like k) with
+                                     //    row-major block sums vc; 0: transposed vt
+                                     //    [B, H, D, Tp] (b, h, d strides) with vct
+  const bf16* v; int64_t v_sb, v_st, v_sh;
+  const bf16* vt; int64_t vt_sb, vt_sh, vt_sd;
+  int B, H, Sq, Sk;                  // Sk: tokens available in k / v (rows >= Sk read as 0)
   int mask_tail;                     // 1: exact-part keys >= Sk take no part (the Triton
                                      // host, triton_kernels.py:185); 0: they are zero keys
                                      // attended with logit 0 (TileLang's zero padding)
@@ -147,7 +153,8 @@ struct SparseParams {
   const int* idx;                    // [BH, n_qblk, top_k] ascending
   int top_k, NKV, NKVp;
   const bf16* kc;                    // [BH, NKVp, D]
-  const bf16* vct;                   // [BH, D, NKVp]
+  const bf16* vc;                    // [BH, NKVp, D]  (v_rows)
+  const bf16* vct;                   // [BH, D, NKVp]  (!v_rows)
   const float* out_c; int nb_q;
   AlphaView alpha;
   OutView out;

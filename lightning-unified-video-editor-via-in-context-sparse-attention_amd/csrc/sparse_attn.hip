@@ -21,19 +21,26 @@
 // what lets two waves share each SIMD.
 //
 // The new KV is read in place: new-KV block j lives at source block kvmap[j] of the
-// (k, vt) buffers -- target blocks and the selected source blocks of the original
+// K / V buffers -- target blocks and the selected source blocks of the original
 // sequence -- or is an all-zero block (kvmap -1 / an out-of-range caller index, the
-// reference's TKV zero padding, attended with logit 0).  KC / VC^T are the bf16 block sums
-// of the new KV.  With mask_tail (the Triton host's ragged TKV) the keys of an exact block
-// at or past Sk get no weight instead (triton_kernels.py:185); the interval part is the
-// same in both modes.
+// reference's TKV zero padding, attended with logit 0).  KC and VC (or VC^T) are the bf16
+// block sums of the new KV.  With mask_tail (the Triton host's ragged TKV)
+// the keys of an exact block at or past Sk get no weight instead (triton_kernels.py:185);
+// the interval part is the same in both modes.
 //
 // Workgroup = 2 waves = one query block (wave w: rows 32 w .. 32 w + 31); four workgroups
-// share a CU.  One K buffer and one V^T buffer per workgroup, filled by direct
+// share a CU.  One K buffer and one V buffer per workgroup, filled by direct
 // global->LDS loads (lane l lands at M0 + 16 l; the XOR swizzle is applied on the global
-// side).  K(t+1) is issued as soon as both waves finished reading K(t) and lands while
-// the softmax and PV of tile t run; V(t+1) is issued after PV(t) and lands during QK and
-// softmax of tile t+1.  The epilogue fuses the residual and the scatter to [B, S, H, D].
+// side).  V comes in one of two layouts (template parameter VROW):
+//   * VROW: 64 rows of the caller's row-major V, a row tile (attn_tile.h) whose PV
+//     operands are formed by transposing LDS reads -- no transposed copy of V is needed
+//     (the sparse host entry points, and the materialised new KV of t % 64 != 0);
+//   * !VROW: a V^T tile (128 d rows of 64 keys in kv_slot order) from the transposed copy
+//     the pipeline's pooling pass already writes for the flash kernel; PV operands are
+//     plain 16-byte reads, which the LDS delivers at a higher rate than transposing ones.
+// K(t+1) is issued as soon as
+// both waves finished reading K(t) and lands while the softmax and PV of tile t run;
+// V(t+1) is issued after PV(t) and lands during QK and softmax of tile t+1.  The epilogue fuses the residual and the scatter to [B, S, H, D].
 // The exact tiles are visited in ascending new-KV order starting at a block that advances
 // with the launch index (a rotation of the list), so that the workgroups resident on one
 // XCD sweep the new KV together.
@@ -48,7 +55,7 @@
 #define SP_BUF_BYTES (SP_STAGE_BYTES > K_TILE_BYTES ? SP_STAGE_BYTES : K_TILE_BYTES)
 #define SP_RESCALE_LOG2 8.0f
 #define SP_PF 2                          // MFMA operand read-ahead (steps); 3 spills at 256 VGPRs
-#define SP_DMA_PER_TILE 8                // LDS-DMA instructions per wave per K or V^T tile
+#define SP_DMA_PER_TILE 8                // LDS-DMA instructions per wave per K or V tile
 #ifndef SP_SWEEP_CONC
 #define SP_SWEEP_CONC 256                // sweep start advances NKV / SP_SWEEP_CONC per launch
 #endif
@@ -57,9 +64,10 @@
 #define SP_WAIT_OLDER() asm volatile("s_waitcnt vmcnt(8)" ::: "memory")
 #define SP_WAIT_ALL() asm volatile("s_waitcnt vmcnt(0)" ::: "memory")
 
+template <bool VROW>
 __global__ void __launch_bounds__(SP_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
 icsa_sparse_kernel(SparseParams p) {
-  // K tile and V^T tile as separate objects, so the compiler can tell a load into one from
+  // K tile and V tile as separate objects, so the compiler can tell a load into one from
   // reads of the other; in the epilogue they hold the fp32 output rows of wave 0 / wave 1.
   __shared__ __attribute__((aligned(16))) unsigned char kbuf[SP_BUF_BYTES];
   __shared__ __attribute__((aligned(16))) unsigned char vbuf[SP_BUF_BYTES];
@@ -112,20 +120,26 @@ icsa_sparse_kernel(SparseParams p) {
                q_valid);
 
   // ---- DMA segments ----
-  // K tile: this wave's rows 32 w .. 32 w + 31 in 8 one-KB segments of 4 rows (segment i:
-  // rows 32 w + 4 i + lane / 16, lane % 16 = physical 16-byte chunk).
-  // V^T tile: d rows 64 w .. 64 w + 63 in 8 segments of 8 rows (d = 64 w + 8 i + lane / 8).
+  // K tiles and V row tiles: this wave's rows 32 w .. 32 w + 31 in 8 one-KB segments of 4
+  // rows (segment i: rows 32 w + 4 i + lane / 16, lane % 16 = physical 16-byte chunk; K
+  // chunks swizzled by row % 16, V chunks by rv_swz).
+  // V^T tiles: d rows 64 w .. 64 w + 63 in 8 segments of 8 rows (d = 64 w + 8 i + lane / 8).
   const bf16* kbase = p.k + (int64_t)b * p.k_sb + (int64_t)h * p.k_sh;
-  const bf16* vtbase = p.vt + (int64_t)b * p.vt_sb + (int64_t)h * p.vt_sh;
+  const bf16* vbase = VROW ? p.v + (int64_t)b * p.v_sb + (int64_t)h * p.v_sh
+                           : p.vt + (int64_t)b * p.vt_sb + (int64_t)h * p.vt_sh;
   const bf16* kcb = p.kc + (int64_t)bh * p.NKVp * ICSA_D;
-  const bf16* vcb = p.vct + (int64_t)bh * ICSA_D * p.NKVp;
-  const int k_row0 = 32 * wave + (lane >> 4);        // key row of K segment 0
+  const bf16* vcb = (VROW ? p.vc : p.vct) + (int64_t)bh * p.NKVp * ICSA_D;
+  const int k_row0 = 32 * wave + (lane >> 4);        // tile row of segment 0
   const int v_row0 = 64 * wave + (lane >> 3);        // d row of V^T segment 0
   int kro[8], vro[4];                                 // MFMA operand read offsets (bytes)
 #pragma unroll
   for (int kk = 0; kk < 8; ++kk) kro[kk] = k_lds_off(li, 2 * kk + hl) * 2;
+  if constexpr (VROW) {
+    rt_tr_offsets<true>(vro, lane);                   // transposing reads of the row tile
+  } else {
 #pragma unroll
-  for (int m = 0; m < 4; ++m) vro[m] = v_lds_off(li, 2 * m + hl) * 2;
+    for (int m = 0; m < 4; ++m) vro[m] = v_lds_off(li, 2 * m + hl) * 2;
+  }
 
   __syncthreads();                                    // src_l / sel_l / rot_l ready
   const int rot = __builtin_amdgcn_readfirstlane(rot_l);
@@ -133,8 +147,9 @@ icsa_sparse_kernel(SparseParams p) {
   auto ex_entry = [&](int g) -> int { return g + rot < top_k ? g + rot : g + rot - top_k; };
 
   // Tile g: g < T1 exact block src_l[g]; T1 <= g < T2 pass-1 chunk g - T1 (K only);
-  // g >= T2 pass-2 chunk g - T2.  issue_k returns the number of real key rows (the rest
-  // are zeroed after the wait); issue_v returns whether the V^T tile is all zeros.
+  // g >= T2 pass-2 chunk g - T2.  issue_k / issue_v return the number of real keys (the
+  // rest are zeroed after the wait; a V^T tile is either all real -- the copy is zero
+  // padded -- or a zero block).
   auto issue_k = [&](int g) -> int {
     const bf16* base;
     int64_t bytes;
@@ -164,49 +179,70 @@ icsa_sparse_kernel(SparseParams p) {
     }
     return valid;
   };
-  auto issue_v = [&](int g) -> bool {
+  auto issue_v = [&](int g) -> int {
     const bf16* base;
     int64_t bytes;
-    bool zero = false;
-    int rs2;                               // V^T row stride in bytes
+    int valid, rs2;                        // rs2: row stride in bytes (V rows / V^T d rows)
     const bool ex = g < T1;
     if (ex) {
       const int src = __builtin_amdgcn_readfirstlane(src_l[ex_entry(g)]);
-      zero = src < 0;
-      base = vtbase + (zero ? 0 : (int64_t)src * ATT_BN);
-      bytes = zero ? 0 : ((int64_t)(ICSA_D - 1) * p.vt_sd + ATT_BN) * 2;
-      rs2 = (int)p.vt_sd * 2;
+      const int tok0 = src * ATT_BN;
+      if constexpr (VROW) {
+        valid = src < 0 ? 0 : min(ATT_BN, p.Sk - tok0);
+        base = vbase + (src < 0 ? 0 : (int64_t)tok0 * p.v_st);
+        bytes = valid > 0 ? ((int64_t)(valid - 1) * p.v_st + ICSA_D) * 2 : 0;
+        rs2 = (int)p.v_st * 2;
+      } else {
+        valid = src < 0 ? 0 : ATT_BN;
+        base = vbase + (src < 0 ? 0 : tok0);
+        bytes = src < 0 ? 0 : ((int64_t)(ICSA_D - 1) * p.vt_sd + ATT_BN) * 2;
+        rs2 = (int)p.vt_sd * 2;
+      }
     } else {
       const int c = g - T2;
-      base = vcb + (int64_t)c * ATT_BN;
-      bytes = ((int64_t)(ICSA_D - 1) * p.NKVp + ATT_BN) * 2;
-      rs2 = p.NKVp * 2;
+      valid = ATT_BN;
+      base = vcb + (int64_t)c * ATT_BN * (VROW ? ICSA_D : 1);
+      bytes = VROW ? (int64_t)ATT_BN * ICSA_D * 2 : ((int64_t)(ICSA_D - 1) * p.NKVp + ATT_BN) * 2;
+      rs2 = VROW ? ICSA_D * 2 : p.NKVp * 2;
     }
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(base, bytes);
     unsigned char* dst = vbuf + wave * 8192;
 #pragma unroll
     for (int i = 0; i < SP_DMA_PER_TILE; ++i) {
-      const int d = v_row0 + 8 * i;
-      const int off = d * rs2 + (((lane & 7) ^ ((d >> 1) & 7)) << 4);
+      int off;
+      if constexpr (VROW) {
+        const int r = k_row0 + 4 * i;
+        off = r * rs2 + (((lane & 15) ^ rv_swz(r)) << 4);
+      } else {
+        const int d = v_row0 + 8 * i;
+        off = d * rs2 + (((lane & 7) ^ ((d >> 1) & 7)) << 4);
+      }
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)(dst + 1024 * i), 16, off, 0, 0, 0);
     }
-    return zero;
+    return valid;
   };
-  // After the wait: zero this wave's K rows >= valid / its whole V^T half (zero blocks).
-  auto fill_k = [&](int valid) {
+  // After the wait: zero this wave's key rows >= valid of the K buffer / a V row tile
+  // (rows past the sequence and zero blocks are zero keys and values).
+  auto fill_rows = [&](unsigned char* buf, int valid) {
     if (valid >= ATT_BN) return;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int r = 32 * wave + 4 * i + (lane >> 4);
-      if (r >= valid) *reinterpret_cast<u32x4*>(kbuf + r * ICSA_D * 2 + (lane & 15) * 16) = u32x4{0u, 0u, 0u, 0u};
+      if (r >= valid)                      // 4-byte stores: one zero register
+        for (int e = 0; e < 4; ++e) *reinterpret_cast<unsigned*>(buf + r * ICSA_D * 2 + (lane & 15) * 16 + 4 * e) = 0u;
     }
   };
-  auto fill_v = [&](bool zero) {
-    if (!zero) return;
+  // ... and this wave's half of a V^T tile of a zero block
+  auto fill_v = [&](int valid) {
+    if constexpr (VROW) {
+      fill_rows(vbuf, valid);
+    } else {
+      if (valid > 0) return;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int d = 64 * wave + 8 * i + (lane >> 3);
-      *reinterpret_cast<u32x4*>(vbuf + d * ATT_BN * 2 + (lane & 7) * 16) = u32x4{0u, 0u, 0u, 0u};
+      for (int i = 0; i < 8; ++i) {
+        const int d = 64 * wave + 8 * i + (lane >> 3);
+        *reinterpret_cast<u32x4*>(vbuf + d * ATT_BN * 2 + (lane & 7) * 16) = u32x4{0u, 0u, 0u, 0u};
+      }
     }
   };
 
@@ -235,21 +271,25 @@ icsa_sparse_kernel(SparseParams p) {
     s[0] = acc0;
     s[1] = acc1;
   };
-  // O^T += V^T P^T for the V^T buffer
+  // O^T += V^T P^T for the V buffer
   auto pv = [&]() {
-    bf16x8 va[16];
+    if constexpr (VROW) {
+      pv_tile_tr<SP_PF, true>(o, vbuf, vro, pf);       // transposing reads of the row tile
+    } else {
+      bf16x8 va[16];
 #pragma unroll
-    for (int t = 0; t < SP_PF; ++t)
-      va[t] = *reinterpret_cast<const bf16x8*>(vbuf + vro[t >> 2] + (t & 3) * 32 * ATT_BN * 2);
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int t = 0; t < 16; ++t) {
-      if (t + SP_PF < 16) {
-        const int u = t + SP_PF;
-        va[u] = *reinterpret_cast<const bf16x8*>(vbuf + vro[u >> 2] + (u & 3) * 32 * ATT_BN * 2);
-      }
-      o[t & 3] = mfma32x32x16(va[t], pf[t >> 2], o[t & 3]);
+      for (int t = 0; t < SP_PF; ++t)
+        va[t] = *reinterpret_cast<const bf16x8*>(vbuf + vro[t >> 2] + (t & 3) * 32 * ATT_BN * 2);
       __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int t = 0; t < 16; ++t) {
+        if (t + SP_PF < 16) {
+          const int u = t + SP_PF;
+          va[u] = *reinterpret_cast<const bf16x8*>(vbuf + vro[u >> 2] + (u & 3) * 32 * ATT_BN * 2);
+        }
+        o[t & 3] = mfma32x32x16(va[t], pf[t >> 2], o[t & 3]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
   };
   auto rescale_o = [&](float a) {
@@ -283,12 +323,12 @@ icsa_sparse_kernel(SparseParams p) {
   float l_run = 0.f;
 
   int kv_pending = issue_k(0);
-  bool vz_pending = issue_v(0);
+  int vv_pending = issue_v(0);
 
   // ---- 1. exact blocks ----
   for (int t = 0; t < T1; ++t) {
     SP_WAIT_OLDER();                       // K(t); V(t) is the newer tile in flight
-    fill_k(kv_pending);
+    fill_rows(kbuf, kv_pending);
     ATT_BARRIER();
     qk();
     ATT_BARRIER();                       // K buffer free
@@ -326,11 +366,11 @@ icsa_sparse_kernel(SparseParams p) {
       }
     l_run += rs;
     SP_WAIT_OLDER();                       // V(t); K(t+1) is the newer tile in flight
-    fill_v(vz_pending);
+    fill_v(vv_pending);
     ATT_BARRIER();
     pv();
     ATT_BARRIER();                       // V buffer free
-    vz_pending = issue_v(t + 1 < T1 ? t + 1 : T2);
+    vv_pending = issue_v(t + 1 < T1 ? t + 1 : T2);
     kv_pending = kv_next;
   }
 
@@ -405,9 +445,14 @@ hipError_t launch_sparse(const SparseParams& p, hipStream_t stream) {
   if (p.NKV < 1 || p.NKV > SP_MAX_CHUNKS * ATT_BN) return hipErrorInvalidValue;
   if (p.NKVp % ATT_BN != 0 || p.NKVp < p.NKV) return hipErrorInvalidValue;
   // per-(b, h) slices must be addressable with 32-bit buffer offsets
-  if ((int64_t)p.Sk * p.k_st * 2 > 0x7fffffffLL || (int64_t)ICSA_D * p.vt_sd * 2 > 0x7fffffffLL ||
-      16LL * p.k_st * 2 > 0x7fffffffLL)
+  if ((int64_t)p.Sk * p.k_st * 2 > 0x7fffffffLL || 64LL * p.k_st * 2 > 0x7fffffffLL)
     return hipErrorInvalidValue;
-  hipLaunchKernelGGL(icsa_sparse_kernel, dim3(xcd_grid(n_work)), dim3(SP_THREADS), 0, stream, p);
+  if (p.v_rows ? ((int64_t)p.Sk * p.v_st * 2 > 0x7fffffffLL || 64LL * p.v_st * 2 > 0x7fffffffLL || !p.vc)
+               : ((int64_t)ICSA_D * p.vt_sd * 2 > 0x7fffffffLL || !p.vct))
+    return hipErrorInvalidValue;
+  if (p.v_rows)
+    hipLaunchKernelGGL(icsa_sparse_kernel<true>, dim3(xcd_grid(n_work)), dim3(SP_THREADS), 0, stream, p);
+  else
+    hipLaunchKernelGGL(icsa_sparse_kernel<false>, dim3(xcd_grid(n_work)), dim3(SP_THREADS), 0, stream, p);
   return hipGetLastError();
 }

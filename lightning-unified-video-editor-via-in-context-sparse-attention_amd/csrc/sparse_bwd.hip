@@ -94,24 +94,14 @@ __global__ void __launch_bounds__(256) icsa_sparse_bwd_sums_kernel(SparseBwdPara
 }
 
 // ------------------------------------------------------------------------------------------
-// Tile DMA.  A 16 KB row tile (64 rows x 128 dims, swizzled by bw_swz below) is 16
+// Tile DMA.  A 16 KB row tile (64 rows x 128 dims, swizzled by rt_swz) is 16
 // LDS-DMA instructions, 8 per wave; each lands 1 KB at consecutive LDS addresses (lane l
 // at +16 l), so the XOR swizzle is applied on the global side.  Loads complete in issue
 // order: with the next step's tiles in flight a kernel waits with vmcnt(their count).
 // ------------------------------------------------------------------------------------------
 #define BW_WAIT(n) asm volatile("s_waitcnt vmcnt(" #n ")" ::: "memory")
 
-// Row-tile swizzle of the backward: 16-byte chunk c of row r sits at slot c ^ bw_swz(r).
-// bw_swz is a bijection of r % 16, so the 16-byte operand reads of 16 consecutive rows
-// (one chunk) hit 16 distinct slots; and it moves rows 4 a + x (x = 0..3) to different slot
-// quadrants, so a transposing read (4 rows x 4 chunk positions x 2 halves per half-wave)
-// touches 32 distinct 8-byte bank pairs.  The forward's swizzle (c ^ (r % 16)) folds those
-// 16 (row, chunk) pairs onto 4 slots.
-__device__ __forceinline__ int bw_swz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
-__device__ __forceinline__ int bw_row_off(int row, int chunk) {    // in bf16 elements
-  return row * ICSA_D + ((chunk ^ bw_swz(row)) << 3);
-}
-
+// Row tiles use the shared layout of attn_tile.h (rt_swz / rt_off).
 #define BW_PF 3                 // MFMA operand read-ahead (steps)
 
 // S^T (or S) for the 64 rows of a backward row tile: s[sub] covers rows 32 sub .. 32 sub + 31.
@@ -121,7 +111,7 @@ __device__ __forceinline__ void qk_tile_bw(floatx16 s[2], const bf16* tile, cons
   const int lane = threadIdx.x & 63;
   const int li = lane & 31, hl = lane >> 5;
   auto ld = [&](int t) -> bf16x8 {
-    return *reinterpret_cast<const bf16x8*>(tile + bw_row_off(32 * (t & 1) + li, 2 * (t >> 1) + hl));
+    return *reinterpret_cast<const bf16x8*>(tile + rt_off(32 * (t & 1) + li, 2 * (t >> 1) + hl));
   };
   bf16x8 a[16];
 #pragma unroll
@@ -146,59 +136,11 @@ __device__ __forceinline__ void bw_dma_rows(unsigned char* tile, const bf16* bas
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int r = 32 * wave + 4 * i + (lane >> 4);
-    const int off = (int)(r * rs * 2) + (((lane & 15) ^ bw_swz(r)) << 4);
+    const int off = (int)(r * rs * 2) + (((lane & 15) ^ rt_swz(r)) << 4);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_ptr)(dst + 1024 * i), 16, off, 0, 0, 0);
   }
 }
 
-// ------------------------------------------------------------------------------------------
-// Transposed MFMA operands straight from a row tile (ds_read_b64_tr_b16).  Within each
-// group of 16 lanes, lane j of the transposing read receives element j % 4 of the 4-element
-// vectors read by lanes j / 4 + 4 e (e = 0..3).  For the A operand of
-// O^T[d][key] += X^T[d][row] P[row][key] (X a 64 x 128 row tile, lane l = 16 g + s holding
-// A[d = 32 ds + l % 32][k = 8 (l / 32) + e]) with the row order of the score accumulators
-// (k -> row 16 m + 8 (e / 4) + 4 (l / 32) + e % 4), lane 16 g + s reads the 4 dims
-// 32 ds + 16 (g % 2) + 4 (s % 4) .. + 3 of row 16 m + 4 (g / 2) + s / 4 (+ 8 for e >= 4).
-// tro[h][ds]: those byte offsets in the row-tile layout for m = 0; step m adds 16 rows.
-// ------------------------------------------------------------------------------------------
-typedef short bw_v4s __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) bw_v4s* bw_lds_v4s;
-
-__device__ __forceinline__ void tr_offsets(int tro[2][4], int lane) {
-  const int g = lane >> 4, s = lane & 15;
-#pragma unroll
-  for (int h = 0; h < 2; ++h)
-#pragma unroll
-    for (int ds = 0; ds < 4; ++ds) {
-      const int row = 4 * (g >> 1) + (s >> 2) + 8 * h;
-      const int col = 32 * ds + 16 * (g & 1) + 4 * (s & 3);
-      tro[h][ds] = row * (ICSA_D * 2) + (((col >> 3) ^ bw_swz(row)) << 4) + (col & 7) * 2;
-    }
-}
-
-// o[4 d-subtiles] += X^T P for a row tile X (bytes at `tile`); p[m]: bf16 B operand of
-// 16-row step m, straight from the score accumulators.  Step t = 4 m + ds; each operand is
-// two transposing reads, issued BW_PF steps ahead.
-__device__ __forceinline__ void pv_tile_tr(floatx16 o[4], const unsigned char* tile, const int tro[2][4],
-                                           const bf16x8 p[4]) {
-  auto ld = [&](int t) -> bf16x8 {
-    const int m = t >> 2, ds = t & 3;
-    const bw_v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((bw_lds_v4s)(tile + tro[0][ds] + m * 16 * ICSA_D * 2));
-    const bw_v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((bw_lds_v4s)(tile + tro[1][ds] + m * 16 * ICSA_D * 2));
-    const short __attribute__((ext_vector_type(8))) a8 = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-    return __builtin_bit_cast(bf16x8, a8);
-  };
-  bf16x8 a[16];
-#pragma unroll
-  for (int t = 0; t < BW_PF; ++t) a[t] = ld(t);
-  __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-  for (int t = 0; t < 16; ++t) {
-    if (t + BW_PF < 16) a[t + BW_PF] = ld(t + BW_PF);
-    o[t & 3] = mfma32x32x16(a[t], p[t >> 2], o[t & 3]);
-    __builtin_amdgcn_sched_barrier(0);
-  }
-}
 
 // ------------------------------------------------------------------------------------------
 // dq: one workgroup per query block.  Steps t = 0 .. n_ex + nc - 1: the valid selected
@@ -243,8 +185,8 @@ __global__ void __launch_bounds__(BW_THREADS) icsa_sparse_bwd_dq_kernel(SparseBw
   load_q_frags(dof, p.dout + (int64_t)b * p.do_sb + (int64_t)h * p.do_sh + (int64_t)qtok0 * p.do_st, p.do_st, 32);
   const float lse = p.lse[(int64_t)bh * p.TQ + qtok0 + li];
   const float dd = p.dvec[(int64_t)bh * p.TQ + qtok0 + li];
-  int tro[2][4];
-  tr_offsets(tro, lane);
+  int tro[4];
+  rt_tr_offsets<false>(tro, lane);
   __syncthreads();
   const int n_ex = *n_ex_l;
   const int T = n_ex + p.nc;
@@ -305,7 +247,7 @@ __global__ void __launch_bounds__(BW_THREADS) icsa_sparse_bwd_dq_kernel(SparseBw
           dsf[2 * sub + (e >> 3)][e & 7] = (bf16)(pr * (dp[sub][e] - 64.0f * dd) * (1.0f / 64.0f));
         }
     }
-    pv_tile_tr(dq, ks, tro, dsf);                      // dQ^T += K^T dS^T
+    pv_tile_tr<BW_PF, false>(dq, ks, tro, dsf);                      // dQ^T += K^T dS^T
     ATT_BARRIER();                                     // buffer t & 1 consumed
   }
 
@@ -366,8 +308,8 @@ __global__ void __launch_bounds__(BW_THREADS) icsa_sparse_bwd_dkv_kernel(SparseB
     load_q_frags(kf, p.k + (int64_t)b * p.k_sb + (int64_t)h * p.k_sh + (int64_t)key0 * p.k_st, p.k_st, 32);
     load_q_frags(vf, p.v + (int64_t)b * p.v_sb + (int64_t)h * p.v_sh + (int64_t)key0 * p.v_st, p.v_st, 32);
   }
-  int tro[2][4];
-  tr_offsets(tro, lane);
+  int tro[4];
+  rt_tr_offsets<false>(tro, lane);
 
   // query blocks to visit, ascending
   int i_begin = 0, i_count;
@@ -447,12 +389,12 @@ __global__ void __launch_bounds__(BW_THREADS) icsa_sparse_bwd_dkv_kernel(SparseB
     auto ld = [&](int t) -> bf16x8 {
       if (t < 32) {
         const int sub = t >> 4, kk = (t & 15) >> 1;
-        return *reinterpret_cast<const bf16x8*>(((t & 1) ? dosb : qsb) + bw_row_off(32 * sub + li, 2 * kk + hl));
+        return *reinterpret_cast<const bf16x8*>(((t & 1) ? dosb : qsb) + rt_off(32 * sub + li, 2 * kk + hl));
       }
       const int u = t - 32, m = u >> 3, ds = (u >> 1) & 3;
       const unsigned char* tile = (u & 1) ? qs : dos;
-      const bw_v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((bw_lds_v4s)(tile + tro[0][ds] + m * 16 * ICSA_D * 2));
-      const bw_v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((bw_lds_v4s)(tile + tro[1][ds] + m * 16 * ICSA_D * 2));
+      const rt_v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((rt_lds_v4s)(tile + tro[ds] + m * 16 * ICSA_D * 2));
+      const rt_v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((rt_lds_v4s)(tile + rt_tr_hi<false>(tro[ds]) + m * 16 * ICSA_D * 2));
       const short __attribute__((ext_vector_type(8))) a8 = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
       return __builtin_bit_cast(bf16x8, a8);
     };

@@ -80,6 +80,14 @@ def test_structured_fp32_inputs_alpha_tensor(gpu):
     _run_case(gpu, q, k, v, t, alpha=alpha)
 
 
+@pytest.mark.parametrize("real,pad", [(2520, 8), (2000, 0)])
+def test_fp32_v(gpu, real, pad):
+    # f32 v (values exact in bf16): the attention stages read the library's bf16 copy of v,
+    # the pooling its f32 values; aligned and unaligned t (the new KV gathered from f32 v)
+    q, k, v, t = make_inputs(H=2, real=real, pad=pad, kind="random", seed=6)
+    _run_case(gpu, q, k, v.float(), t)
+
+
 def test_unaligned_target_and_partial_last_block(gpu):
     # t % 64 != 0 (new-KV blocks straddle source blocks) and S % 64 != 0
     q, k, v, t = make_inputs(H=2, real=2000, pad=0, kind="random", seed=4)

@@ -66,6 +66,14 @@ def test_workspace_layout_is_aligned_and_disjoint():
         o = list(offs)
         assert all(x % 256 == 0 and 0 <= x <= total for x in o)
         assert o == sorted(o)
+    # block sums of the new v: transposed for the V^T tiles of aligned t, row-major for the
+    # row tiles of the materialised new KV (t % 64 != 0); no transposed copy of the new V
+    vc, vct = _lib.WS_SLOTS.index("VC"), _lib.WS_SLOTS.index("VCT")
+    for t, want_vc in ((32768, False), (32760, True)):
+        offs = (ctypes.c_int64 * n)()
+        L.icsa_editing_workspace_layout(1, 65536, 40, 128, t, 0.0625, 0.125, 0.5, _lib.BF16, _lib.BF16,
+                                        ctypes.cast(offs, ctypes.c_void_p))
+        assert (offs[vc + 1] > offs[vc]) == want_vc and (offs[vct + 1] > offs[vct]) != want_vc
 
 
 def _status(name, *args):
