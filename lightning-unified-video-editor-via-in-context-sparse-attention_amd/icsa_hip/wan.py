@@ -371,9 +371,18 @@ class WanAttentionBlock(nn.Module):
         ones = torch.ones(x.shape[0], self.dim, device=x.device)
         h = ln_modulate(x, y=y.to(torch.bfloat16), gate=ones, shift=em[3], scale=em[4],
                         eps=self.eps)                                # x += cross, norm2, modulate
-        y = self.ffn(h)
+        y = self._ffn(h)
         ln_modulate(x, y=y.to(torch.bfloat16), gate=em[5], out=False)   # x += ffn e5
         return x
+
+    def _ffn(self, h):
+        """self.ffn(h) (Linear, GELU(tanh), Linear; model.py:243-245) with the bias and the
+        GELU applied in the first GEMM's epilogue, on its fp32 accumulator: no separate
+        elementwise pass over the [tokens, ffn_dim] hidden.  The reference rounds the first
+        Linear's output to bf16 before its GELU; the epilogue rounds once, after it."""
+        lin0, lin2 = self.ffn[0], self.ffn[2]
+        f = torch._addmm_activation(lin0.bias, h.reshape(-1, h.shape[-1]), lin0.weight.t(), use_gelu=True)
+        return torch.nn.functional.linear(f, lin2.weight, lin2.bias).view(*h.shape[:-1], lin2.out_features)
 
 
 def sinusoidal_embedding_1d(dim, position):
