@@ -129,17 +129,36 @@ __global__ void __launch_bounds__(256) icsa_compressed_logits_kernel(CompressedP
 // ---------------------------------------------------------------------------------------
 __device__ __forceinline__ int wave_count(bool pred) { return __popcll(__ballot(pred)); }
 
-// Largest key lo with count(key >= lo) >= k over the wave's VPL keys per lane (keys 0 =
-// absent; requires at least k nonzero keys): the key of the k-th largest.
+// Largest key lo with count(key >= lo) >= k over the wave's keys (keys 0 = absent; requires
+// at least k nonzero keys): the key of the k-th largest.  Only registers u < nu can hold
+// nonzero keys.  Bisection over the key range; as soon as a midpoint has exactly k keys at
+// or above it, the answer is the smallest of those keys (one wave minimum), which for
+// spread-out values ends the search long before the 32nd step.
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t x) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const uint32_t y = (uint32_t)__shfl_xor((int)x, o, 64);
+    x = y < x ? y : x;
+  }
+  return x;
+}
 template <int VPL>
-__device__ __forceinline__ uint32_t kth_largest_key(const uint32_t (&key)[VPL], int k) {
+__device__ __forceinline__ uint32_t kth_largest_key(const uint32_t (&key)[VPL], int k, int nu) {
   uint32_t lo = 0u, hi = 0xffffffffu;
   while (hi - lo > 1u) {
     const uint32_t mid = lo + ((hi - lo) >> 1);
     int c = 0;
 #pragma unroll
-    for (int u = 0; u < VPL; ++u) c += wave_count(key[u] >= mid);
-    if (c >= k) lo = mid; else hi = mid;
+    for (int u = 0; u < VPL; ++u)
+      if (u < nu) c += wave_count(key[u] >= mid);
+    if (c == k) {
+      uint32_t mn = 0xffffffffu;
+#pragma unroll
+      for (int u = 0; u < VPL; ++u)
+        if (u < nu && key[u] >= mid && key[u] < mn) mn = key[u];
+      return wave_min_u32(mn);
+    }
+    if (c > k) lo = mid; else hi = mid;
   }
   return lo;
 }
@@ -170,7 +189,7 @@ __global__ void __launch_bounds__(256) icsa_compressed_stats_kernel(CompressedPa
 #pragma unroll
     for (int u = 0; u < VPL; ++u) key[u] = lane + 64 * u < n_t ? f2key(v[u]) : 0u;
     const int k = p.k_sparsity;
-    const uint32_t lo = kth_largest_key<VPL>(key, k);
+    const uint32_t lo = kth_largest_key<VPL>(key, k, (n_t + 63) / 64);
     int cgt = 0;
     float sa = 0.f;
 #pragma unroll
@@ -487,7 +506,7 @@ __global__ void __launch_bounds__(256) icsa_level3_select_kernel(Level3Params p)
     const int j = lane + 64 * u;
     key[u] = j < NKV ? f2key(srow[j]) : 0u;         // 0 is below every real key
   }
-  const uint32_t lo = kth_largest_key<VPL>(key, k);
+  const uint32_t lo = kth_largest_key<VPL>(key, k, (NKV + 63) / 64);
   int cgt = 0;
 #pragma unroll
   for (int u = 0; u < VPL; ++u) cgt += wave_count(key[u] > lo);
