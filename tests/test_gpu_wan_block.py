@@ -158,3 +158,41 @@ def test_block_full_width_cfg4(gpu):
           flush=True)
     assert torch.isfinite(out).all()
     assert mx <= 3e-2 and mn <= 3e-3, (mx, mn)
+
+
+def test_block_full_width_cfg5(gpu):
+    """Configuration 5's block at full width for one video of the CFG pair: dim 5120, 40
+    heads, FFN 13,824, 21x45x80 target and source grids (151,200 tokens: NB = 2,363,
+    NKV = 1,329, top_k = 83), 512 text tokens.  Float64 oracle on the GPU, the block's own
+    self-attention decisions."""
+    dim, ffn, H = 5120, 13824, 40
+    grid = (21, 45, 80)
+    S = 2 * math.prod(grid)
+    print(f"[block-cfg5] dim={dim} ffn={ffn} H={H} S={S}", flush=True)
+    P = _params_full(dim, ffn, 6, gpu)
+    blk = wan.WanAttentionBlock("t2v_cross_attn", dim, ffn, H, cross_attn_norm=True)
+    blk.load_state_dict({k: v.float().cpu() for k, v in P.items()}, strict=True)
+    blk = blk.to(gpu).to(torch.bfloat16)
+    del P
+    g = torch.Generator(device=gpu).manual_seed(13)
+    x = torch.randn(1, S, dim, generator=g, device=gpu)
+    e = torch.randn(1, 6, dim, generator=g, device=gpu) * 0.1
+    ctx = torch.randn(1, 512, dim, generator=g, device=gpu).to(torch.bfloat16)
+    freqs = W.wan_freqs(128)
+    blk.self_attn.capture = {}
+    out = blk(x.clone(), e, torch.tensor([S]), [grid], freqs, ctx, None, [grid], 1)
+    torch.cuda.synchronize()
+    dec = gpu_decisions(blk.self_attn.capture["views"])
+    blk.self_attn.capture = None
+    Pb = {k: v.detach() for k, v in blk.state_dict().items()}
+    del blk
+    torch.cuda.empty_cache()
+    print("[block-cfg5] HIP block done; float64 oracle on the GPU", flush=True)
+    ref, info = WB.wan_block_forward(Pb, x, e, ctx, grid, grid, 1, freqs, H, decisions=dec, device=gpu)
+    torch.cuda.synchronize()
+    d = (out.double() - ref).abs()
+    mx, mn = d.max().item(), d.mean().item()
+    print(f"[block-cfg5] max_abs={mx:.3e} mean_abs={mn:.3e} |x|max={ref.abs().max().item():.2f}",
+          flush=True)
+    assert torch.isfinite(out).all()
+    assert mx <= 3e-2 and mn <= 3e-3, (mx, mn)
