@@ -467,15 +467,27 @@ __global__ void __launch_bounds__(128) icsa_level3_scores_kernel(Level3Params p)
   }
   const float* kc = p.kc32 + (int64_t)bh * NKV * ICSA_D;
   float* sc = p.scores + ((int64_t)bh * p.n_rows + r_base) * NKV;
+  // the next chunk's 64 rows are loaded into registers (16 float4 per thread) while the
+  // current chunk is multiplied
+  floatx4 kpre[16];
+  auto load_chunk = [&](int k0) {
+#pragma unroll
+    for (int x = 0; x < 16; ++x) {
+      const int e = threadIdx.x + 128 * x, r = e >> 5, c4 = e & 31;
+      kpre[x] = k0 + r < NKV ? *reinterpret_cast<const floatx4*>(kc + (int64_t)(k0 + r) * ICSA_D + 4 * c4)
+                             : floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+  };
+  load_chunk(0);
   for (int k0 = 0; k0 < NKV; k0 += 64) {
     __syncthreads();                              // q rows ready / previous chunk consumed
-    for (int e = threadIdx.x; e < 64 * 32; e += 128) {
-      const int r = e >> 5, c4 = e & 31;
-      floatx4 kv = {0.f, 0.f, 0.f, 0.f};
-      if (k0 + r < NKV) kv = *reinterpret_cast<const floatx4*>(kc + (int64_t)(k0 + r) * ICSA_D + 4 * c4);
-      *reinterpret_cast<floatx4*>(&ks[r][4 * c4]) = kv;
+#pragma unroll
+    for (int x = 0; x < 16; ++x) {
+      const int e = threadIdx.x + 128 * x, r = e >> 5, c4 = e & 31;
+      *reinterpret_cast<floatx4*>(&ks[r][4 * c4]) = kpre[x];
     }
     __syncthreads();
+    if (k0 + 64 < NKV) load_chunk(k0 + 64);
     floatx16 acc = {};
 #pragma unroll 4
     for (int kk = 0; kk < 64; kk += 4) {
