@@ -129,33 +129,68 @@ __global__ void __launch_bounds__(256) icsa_compressed_logits_kernel(CompressedP
 // ---------------------------------------------------------------------------------------
 __device__ __forceinline__ int wave_count(bool pred) { return __popcll(__ballot(pred)); }
 
+// Whole-wave reductions over DPP lane moves (no LDS round trip): quad swaps, half-row and
+// row mirrors leave every lane of a 16-lane row holding the row's result; two row
+// broadcasts fold rows 0+1 and 2+3 and then the pairs into lane 63, which is read back as
+// a wave-uniform value.  A fixed combination order, so sums are bitwise reproducible.
+// Every lane of the wave must be active.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ uint32_t dpp_mov(uint32_t old, uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)old, (int)x, CTRL, ROWS, 0xf, false);
+}
+template <typename F>
+__device__ __forceinline__ uint32_t wave_reduce(uint32_t x, uint32_t ident, F op) {
+  x = op(x, dpp_mov<0xb1, 0xf>(ident, x));     // quad_perm [1, 0, 3, 2]
+  x = op(x, dpp_mov<0x4e, 0xf>(ident, x));     // quad_perm [2, 3, 0, 1]
+  x = op(x, dpp_mov<0x141, 0xf>(ident, x));    // row_half_mirror
+  x = op(x, dpp_mov<0x140, 0xf>(ident, x));    // row_mirror
+  x = op(x, dpp_mov<0x142, 0xa>(ident, x));    // row_bcast:15 into rows 1 and 3
+  x = op(x, dpp_mov<0x143, 0xc>(ident, x));    // row_bcast:31 into rows 2 and 3
+  return (uint32_t)__builtin_amdgcn_readlane((int)x, 63);
+}
+__device__ __forceinline__ float wave_max_dpp(float x) {
+  return __uint_as_float(wave_reduce(__float_as_uint(x), __float_as_uint(-INFINITY), [](uint32_t a, uint32_t b) {
+    return __float_as_uint(fmaxf(__uint_as_float(a), __uint_as_float(b)));
+  }));
+}
+__device__ __forceinline__ float wave_sum_dpp(float x) {
+  return __uint_as_float(wave_reduce(__float_as_uint(x), 0u, [](uint32_t a, uint32_t b) {
+    return __float_as_uint(__uint_as_float(a) + __uint_as_float(b));
+  }));
+}
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t x) {
+  return wave_reduce(x, 0xffffffffu, [](uint32_t a, uint32_t b) { return a < b ? a : b; });
+}
+
 // Largest key lo with count(key >= lo) >= k over the wave's keys (keys 0 = absent; requires
 // at least k nonzero keys): the key of the k-th largest.  Only registers u < nu can hold
-// nonzero keys.  Bisection over the key range; as soon as a midpoint has exactly k keys at
-// or above it, the answer is the smallest of those keys (one wave minimum), which for
-// spread-out values ends the search long before the 32nd step.
-__device__ __forceinline__ uint32_t wave_min_u32(uint32_t x) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) {
-    const uint32_t y = (uint32_t)__shfl_xor((int)x, o, 64);
-    x = y < x ? y : x;
-  }
-  return x;
-}
+// nonzero keys; they are visited in groups of four (one uniform branch per group, the
+// zero keys of a partly used group never count).  Bisection over the key range; as soon
+// as a midpoint has exactly k keys at or above it, the answer is the smallest of those
+// keys (one wave minimum), which for spread-out values ends the search long before the
+// 32nd step.
 template <int VPL>
 __device__ __forceinline__ uint32_t kth_largest_key(const uint32_t (&key)[VPL], int k, int nu) {
+  static_assert(VPL % 4 == 0, "registers are visited in groups of four");
   uint32_t lo = 0u, hi = 0xffffffffu;
   while (hi - lo > 1u) {
     const uint32_t mid = lo + ((hi - lo) >> 1);
     int c = 0;
 #pragma unroll
-    for (int u = 0; u < VPL; ++u)
-      if (u < nu) c += wave_count(key[u] >= mid);
+    for (int g = 0; g < VPL; g += 4)
+      if (g < nu) {
+#pragma unroll
+        for (int u = g; u < g + 4; ++u) c += wave_count(key[u] >= mid);
+      }
     if (c == k) {
       uint32_t mn = 0xffffffffu;
 #pragma unroll
-      for (int u = 0; u < VPL; ++u)
-        if (u < nu && key[u] >= mid && key[u] < mn) mn = key[u];
+      for (int g = 0; g < VPL; g += 4)
+        if (g < nu) {
+#pragma unroll
+          for (int u = g; u < g + 4; ++u)
+            if (key[u] >= mid && key[u] < mn) mn = key[u];
+        }
       return wave_min_u32(mn);
     }
     if (c > k) lo = mid; else hi = mid;
@@ -171,34 +206,41 @@ __global__ void __launch_bounds__(256) icsa_compressed_stats_kernel(CompressedPa
   const int NB = p.NB, n_t = p.n_t;
   const float* L = p.P + row * NB;
   float v[VPL];
+  uint32_t key[VPL];                              // order keys of the target logits (0: none)
   float m = -INFINITY;
 #pragma unroll
   for (int u = 0; u < VPL; ++u) {
     const int j = lane + 64 * u;
     v[u] = j < NB ? L[j] : -INFINITY;
+    key[u] = j < n_t ? f2key(v[u]) : 0u;
     m = fmaxf(m, v[u]);
   }
-  m = wave_max(m);
+  m = wave_max_dpp(m);
   float z = 0.f;
 #pragma unroll
-  for (int u = 0; u < VPL; ++u) z += expf(v[u] - m);
-  z = wave_sum(z);
+  for (int u = 0; u < VPL; ++u) {
+    v[u] = expf(v[u] - m);                        // v now holds exp(L - m)
+    z += v[u];
+  }
+  z = wave_sum_dpp(z);
   float sharp = 0.f;
   if (n_t > 0) {
-    uint32_t key[VPL];
-#pragma unroll
-    for (int u = 0; u < VPL; ++u) key[u] = lane + 64 * u < n_t ? f2key(v[u]) : 0u;
     const int k = p.k_sparsity;
-    const uint32_t lo = kth_largest_key<VPL>(key, k, (n_t + 63) / 64);
+    const int nu = (n_t + 63) / 64;
+    const uint32_t lo = kth_largest_key<VPL>(key, k, nu);
     int cgt = 0;
     float sa = 0.f;
 #pragma unroll
-    for (int u = 0; u < VPL; ++u) {
-      const bool in = key[u] > lo;
-      cgt += wave_count(in);
-      sa += in ? expf(v[u] - m) : 0.f;
-    }
-    sa = wave_sum(sa);
+    for (int g = 0; g < VPL; g += 4)
+      if (g < nu) {
+#pragma unroll
+        for (int u = g; u < g + 4; ++u) {
+          const bool in = key[u] > lo;
+          cgt += wave_count(in);
+          sa += in ? v[u] : 0.f;
+        }
+      }
+    sa = wave_sum_dpp(sa);
     sharp = (sa + (float)(k - cgt) * expf(key2f(lo) - m)) / z;
   }
   if (lane == 0) {
@@ -518,28 +560,37 @@ __global__ void __launch_bounds__(256) icsa_level3_select_kernel(Level3Params p)
     const int j = lane + 64 * u;
     key[u] = j < NKV ? f2key(srow[j]) : 0u;         // 0 is below every real key
   }
-  const uint32_t lo = kth_largest_key<VPL>(key, k, (NKV + 63) / 64);
+  const int nu = (NKV + 63) / 64;
+  const uint32_t lo = kth_largest_key<VPL>(key, k, nu);
   int cgt = 0;
 #pragma unroll
-  for (int u = 0; u < VPL; ++u) cgt += wave_count(key[u] > lo);
+  for (int g = 0; g < VPL; g += 4)
+    if (g < nu) {
+#pragma unroll
+      for (int u = g; u < g + 4; ++u) cgt += wave_count(key[u] > lo);
+    }
   const int need_eq = k - cgt;
   const unsigned long long lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
   int seen_eq = 0, taken = 0;
   int* out = p.idx + row * k;
 #pragma unroll
-  for (int u = 0; u < VPL; ++u) {
-    const int j = lane + 64 * u;
-    const bool gt = key[u] > lo;
-    const bool eq = key[u] == lo && j < NKV;
-    const unsigned long long eqm = __ballot(eq);
-    const int eq_before = seen_eq + __popcll(eqm & lt_mask);
-    const bool take = gt || (eq && eq_before < need_eq);
-    const unsigned long long tm = __ballot(take);
-    const int pos = taken + __popcll(tm & lt_mask);
-    if (take && pos < k) out[pos] = j;
-    seen_eq += __popcll(eqm);
-    taken += __popcll(tm);
-  }
+  for (int g = 0; g < VPL; g += 4)
+    if (g < nu) {
+#pragma unroll
+      for (int u = g; u < g + 4; ++u) {
+        const int j = lane + 64 * u;
+        const bool gt = key[u] > lo;
+        const bool eq = key[u] == lo && j < NKV;
+        const unsigned long long eqm = __ballot(eq);
+        const int eq_before = seen_eq + __popcll(eqm & lt_mask);
+        const bool take = gt || (eq && eq_before < need_eq);
+        const unsigned long long tm = __ballot(take);
+        const int pos = taken + __popcll(tm & lt_mask);
+        if (take && pos < k) out[pos] = j;
+        seen_eq += __popcll(eqm);
+        taken += __popcll(tm);
+      }
+    }
 }
 
 hipError_t launch_level3(const Level3Params& p, hipStream_t stream) {
