@@ -553,12 +553,13 @@ def main():
     exec_flops = fa_flops + sparse_flops + comp_flops
 
     # stage 1: the algorithmic bytes are read q, k, v + write the fp32 sums (the reference's
-    # pooling, 2.076 GB at configuration 2); this pass also writes the V^T copy the flash
-    # kernel reads (reported separately as pool_moved).  Stage 2: read sums, write P once,
-    # write out_c (the algorithmic minimum of the compressed stage).
-    BH, NB, Sp = B * H, z["NB"], z["NB"] * 64
+    # pooling, 2.076 GB at configuration 2); this pass also writes V^T of the target blocks
+    # for the attention kernels (reported separately as pool_moved; the selected source
+    # blocks are transposed after the selection).  Stage 2: read sums, write P once, write
+    # out_c (the algorithmic minimum of the compressed stage).
+    BH, NB = B * H, z["NB"]
     pool_bytes = 3 * B * S * H * D * 2 + 3 * BH * NB * D * 4
-    pool_moved = pool_bytes + BH * D * Sp * 2
+    pool_moved = pool_bytes + BH * D * (-(-t // 64) * 64) * 2
     comp_bytes = 3 * BH * NB * D * 4 + BH * NB * NB * 4 + BH * NB * D * 4
 
     # KV gather (materialised new KV of the drop-in path) on this call's selection

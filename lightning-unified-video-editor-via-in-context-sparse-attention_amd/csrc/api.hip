@@ -254,6 +254,9 @@ int editing_impl(ICSA_EDITING_ARGS, void* const* stage_events, const float* qsum
   pp.vt = reinterpret_cast<bf16*>(WS(ICSA_WS_VT));
   pp.vt_sb = (int64_t)H * ICSA_D * Sp; pp.vt_sh = ICSA_D * Sp; pp.vt_sd = Sp;
   pp.vt_src = 2;
+  // V^T is read only at the target tiles and the selected source blocks: the pooling pass
+  // transposes the target blocks, the selected ones are transposed after the selection
+  pp.vt_limit = 1; pp.vt_nblk = ceil_div(t_seq_len, ICSA_BLOCK);
   pp.B = B; pp.S = S; pp.H = H; pp.NB = z.NB;
   ICSA_HIP_TRY(mark(ICSA_STAGE_START), "event");
   ICSA_HIP_TRY(launch_pool(pp, stream), "pool");
@@ -301,6 +304,7 @@ int editing_impl(ICSA_EDITING_ARGS, void* const* stage_events, const float* qsum
   sp.inject_sel = inject_sel ? 1 : 0;
   sp.inject_order = inject_order ? 1 : 0;
   ICSA_HIP_TRY(launch_select(sp, stream), "select");
+  ICSA_HIP_TRY(launch_vt_blocks(pp, sel, z.n_t, std::max(z.topK, 1), z.topK, stream), "V^T of the selected blocks");
 
   // ---- new-KV block sums (in place for aligned t, materialised otherwise) ----
   NewKvSumsParams np;

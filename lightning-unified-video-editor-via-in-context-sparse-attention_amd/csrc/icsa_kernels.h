@@ -13,9 +13,14 @@ struct PoolParams {
   bf16* vt;             // transposed copy of x[vt_src] (nullptr -> skipped)
   int64_t vt_sb, vt_sh, vt_sd;
   int vt_src;
+  int vt_limit, vt_nblk;  // vt_limit: only blocks n < vt_nblk are transposed
   int B, S, H, NB;      // S tokens, NB = ceil(S / 64) blocks
 };
 hipError_t launch_pool(const PoolParams& p, hipStream_t stream);
+// V^T of a list of blocks only: block base + list[bh * stride + r], r < n, of x[vt_src]
+// (the selected source blocks, transposed after the selection)
+hipError_t launch_vt_blocks(const PoolParams& p, const int* list, int base, int stride, int n,
+                            hipStream_t stream);
 
 // ---------------------------------------------------------------- stage 2 (compressed.hip)
 struct CompressedParams {

@@ -52,6 +52,27 @@ __device__ __forceinline__ void pool_load(const PoolParams& p, int i, int n, int
   }
 }
 
+// V^T of block n from the staged rows vtile[token][d]: thread -> (d, half), 32 consecutive
+// slots of V^T row d, in kv_slot order
+__device__ __forceinline__ void vt_store(const PoolParams& p, int n, int b, int h,
+                                         const bf16 (*vtile)[ICSA_D + 8]) {
+  const int t = threadIdx.x;
+  const int d = t >> 1;
+  const int half = t & 1;
+  bf16* dst = p.vt + (int64_t)b * p.vt_sb + (int64_t)h * p.vt_sh + (int64_t)d * p.vt_sd
+              + (int64_t)n * ICSA_BLOCK + 32 * half;
+#pragma unroll
+  for (int q4 = 0; q4 < 4; ++q4) {
+    bf16x8 o;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int slot = 32 * half + 8 * q4 + e;
+      o[e] = vtile[kv_slot(slot)][d];
+    }
+    *reinterpret_cast<bf16x8*>(dst + 8 * q4) = o;
+  }
+}
+
 template <typename T>
 __device__ __forceinline__ void pool_one(const PoolParams& p, int i, int n, int b, int h, const Raw8<T> (&rows)[4],
                                          float (*red)[ICSA_D + 4], bf16 (*vtile)[ICSA_D + 8]) {
@@ -62,7 +83,7 @@ __device__ __forceinline__ void pool_one(const PoolParams& p, int i, int n, int 
 #pragma unroll
   for (int e = 0; e < 8; ++e) acc[e] = 0.f;
   const bool want_copy = p.xb[i] != nullptr;
-  const bool want_vt = (p.vt != nullptr) && (i == p.vt_src);
+  const bool want_vt = (p.vt != nullptr) && (i == p.vt_src) && !(p.vt_limit && n >= p.vt_nblk);
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int r = g + 16 * j;
@@ -90,23 +111,7 @@ __device__ __forceinline__ void pool_one(const PoolParams& p, int i, int n, int 
     for (int gg = 0; gg < 16; ++gg) s += red[gg][t];      // fixed order: deterministic
     p.sums[i][(((int64_t)b * p.H + h) * p.NB + n) * ICSA_D + t] = s;
   }
-  if (want_vt) {
-    // thread -> (d, half): 32 consecutive slots of Vt row d for this block
-    const int d = t >> 1;
-    const int half = t & 1;
-    bf16* dst = p.vt + (int64_t)b * p.vt_sb + (int64_t)h * p.vt_sh + (int64_t)d * p.vt_sd
-                + (int64_t)n * ICSA_BLOCK + 32 * half;
-#pragma unroll
-    for (int q4 = 0; q4 < 4; ++q4) {
-      bf16x8 o;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int slot = 32 * half + 8 * q4 + e;
-        o[e] = vtile[kv_slot(slot)][d];
-      }
-      *reinterpret_cast<bf16x8*>(dst + 8 * q4) = o;
-    }
-  }
+  if (want_vt) vt_store(p, n, b, h, vtile);
   __syncthreads();
 }
 
@@ -151,5 +156,39 @@ hipError_t launch_pool(const PoolParams& p, hipStream_t stream) {
 #undef ICSA_POOL_CASE
     default: return hipErrorInvalidValue;
   }
+  return hipGetLastError();
+}
+
+// V^T of listed blocks: one workgroup per (b*h, list entry)
+template <typename T>
+__global__ void __launch_bounds__(256) icsa_vt_blocks_kernel(PoolParams p, const int* list, int base,
+                                                             int stride) {
+  __shared__ bf16 vtile[ICSA_BLOCK][ICSA_D + 8];
+  const int bh = blockIdx.x, r = blockIdx.y;
+  const int b = bh / p.H, h = bh % p.H;
+  const int n = base + list[(int64_t)bh * stride + r];
+  if (n < 0 || n >= p.NB) return;                  // uniform for the workgroup
+  Raw8<T> rows[4];
+  pool_load<T>(p, p.vt_src, n, b, h, rows);
+  const int c = threadIdx.x & 15, g = threadIdx.x >> 4;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    float v[8];
+    rows[j].to_f32(v);
+    *reinterpret_cast<bf16x8*>(&vtile[g + 16 * j][8 * c]) = pack8_bf16(v);
+  }
+  __syncthreads();
+  vt_store(p, n, b, h, vtile);
+}
+
+hipError_t launch_vt_blocks(const PoolParams& p, const int* list, int base, int stride, int n,
+                            hipStream_t stream) {
+  if (n <= 0 || p.B * p.H == 0) return hipSuccess;
+  if (!p.vt || !p.x[p.vt_src].p) return hipErrorInvalidValue;
+  dim3 grid(p.B * p.H, n);
+  if (p.x[p.vt_src].dtype == ICSA_DT_F32)
+    hipLaunchKernelGGL(icsa_vt_blocks_kernel<float>, grid, dim3(256), 0, stream, p, list, base, stride);
+  else
+    hipLaunchKernelGGL(icsa_vt_blocks_kernel<bf16>, grid, dim3(256), 0, stream, p, list, base, stride);
   return hipGetLastError();
 }
