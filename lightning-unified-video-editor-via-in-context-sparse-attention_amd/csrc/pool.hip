@@ -6,7 +6,10 @@
 // One workgroup per (b*h, 64-token block), heads fastest.  Each input is read exactly once:
 //   * fp32 block sums        -> sums[i]  [B, H, NB, D]   (means = sums / block size)
 //   * optional bf16 copy     -> xb[i]    same strides as a contiguous [B, S, H, D]
-//   * optional V transposed  -> vt       [B, H, D, Sp] bf16, kv_slot() order, zero padded
+//   * optional V transposed  -> vt       [B, H, D, Sp] bf16, kv_slot() order, zero padded;
+//     with vt_limit only blocks n < vt_nblk (the pipeline's target blocks), and
+//     icsa_vt_blocks_kernel transposes a list of further blocks (the selected source
+//     blocks) once the selection is known
 // Token rows at or beyond S read as zeros, so the partial last block sums only real tokens
 // and the transposed copy is zero for padding tokens.
 #include "icsa_kernels.h"
