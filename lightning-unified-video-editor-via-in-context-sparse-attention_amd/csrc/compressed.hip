@@ -22,20 +22,35 @@ __device__ __forceinline__ float block_size_f(int blk, int NB, int S) {
 }
 
 // ---------------------------------------------------------------------------------------
-// (a) logits L = (Qs/size) (Ks/size)^T / sqrt(D) with fp32 MFMA (32x32x2).  Workgroup =
-//     4 waves = 128 query rows (wave w: rows 32 w .. 32 w + 31) against one of LG_SPLIT
-//     column ranges.  A wave's A operands stay in registers for the whole range (lane
-//     (li, hl) holds row li's dims 64 hl .. 64 hl + 63); 32-column K tiles pass through a
-//     double-buffered LDS ring, the next tile prefetched into registers while the current
-//     one is multiplied.  MFMA step kk contracts dims kk and 64 + kk, kk ascending: a fixed
-//     order, so repeated runs are bitwise identical.
+// (a) logits L = (Qs/size) (Ks/size)^T / sqrt(D) at fp32 accuracy on the bf16 matrix pipe.
+//     Every fp32 operand x is split exactly into three bf16 parts, x = xh + xm + xl + r with
+//     |r| <= 2^-27 |x| (xh = bf16(x), xm = bf16(x - xh), xl = bf16(x - xh - xm)), and each
+//     product is formed from the six part products down to 2^-18 of its size
+//     (al bh + am bm + ah bl + am bh + ah bm + ah bh, small terms first); the dropped
+//     ones are below 2^-25 of it, and every part product is exact in the fp32
+//     accumulator.  So the logits carry fp32-level rounding while the matrix work takes
+//     6 bf16 MFMAs (32x32x16, 32 cycles) per 16 dims instead of 8 fp32 ones (32x32x2, 64).
+//     Workgroup = 4 waves = 128 query rows (wave w: rows 32 w .. 32 w + 31) against one of
+//     LG_SPLIT column ranges.  A wave's split A operands stay in registers for the whole
+//     range (lane (li, hl) holds row li's dims 16 s + 8 hl .. + 7, s = 0 .. 7); 32-column K
+//     tiles pass through a double-buffered LDS ring of split tiles, the next tile prefetched
+//     into registers while the current one is multiplied.  A fixed order of MFMAs, so
+//     repeated runs are bitwise identical.
 // ---------------------------------------------------------------------------------------
 #define LG_SPLIT 4
 #define LG_ROWS 128
 #define LG_COLS 32
+#define LG_KST 136            // bf16 row stride of a split K tile (272 B: conflict-free reads)
+
+__device__ __forceinline__ void split3_bf16(float x, bf16& h, bf16& m, bf16& l) {
+  h = f2bf(x);
+  const float r1 = x - bf2f(h);
+  m = f2bf(r1);
+  l = f2bf(r1 - bf2f(m));
+}
 
 __global__ void __launch_bounds__(256) icsa_compressed_logits_kernel(CompressedParams p) {
-  __shared__ float ks[2][LG_COLS][132];
+  __shared__ __attribute__((aligned(16))) bf16 ks[2][3][LG_COLS][LG_KST];
   const int rt = blockIdx.x, cs = blockIdx.y, bh = blockIdx.z;
   const int NB = p.NB;
   const int tid = threadIdx.x, w = tid >> 6, l = tid & 63;
@@ -43,22 +58,28 @@ __global__ void __launch_bounds__(256) icsa_compressed_logits_kernel(CompressedP
   const float* qbase = p.qsum + (int64_t)bh * NB * ICSA_D;
   const float* kbase = p.ksum + (int64_t)bh * NB * ICSA_D;
 
-  // A operands: this lane's query row, dims 64 hl .. 64 hl + 63, divided by the block size
-  float a[64];
+  // A operands: this lane's query row, divided by the block size, split in three parts
+  bf16x8 ah[8], am[8], al[8];
   {
     const int row = rt * LG_ROWS + 32 * w + li;
-    if (row < NB) {
-      const float sz = block_size_f(row, NB, p.S);
-      const float* src = qbase + (int64_t)row * ICSA_D + 64 * hl;
+    const bool ok = row < NB;
+    const float sz = ok ? block_size_f(row, NB, p.S) : 1.f;
+    const float* src = qbase + (int64_t)(ok ? row : 0) * ICSA_D + 8 * hl;
 #pragma unroll
-      for (int c4 = 0; c4 < 16; ++c4) {
-        const floatx4 v = *reinterpret_cast<const floatx4*>(src + 4 * c4);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) a[4 * c4 + e] = v[e] / sz;
+    for (int st = 0; st < 8; ++st) {
+      floatx4 v0 = {0.f, 0.f, 0.f, 0.f}, v1 = v0;
+      if (ok) {
+        v0 = *reinterpret_cast<const floatx4*>(src + 16 * st);
+        v1 = *reinterpret_cast<const floatx4*>(src + 16 * st + 4);
       }
-    } else {
 #pragma unroll
-      for (int kk = 0; kk < 64; ++kk) a[kk] = 0.f;
+      for (int e = 0; e < 8; ++e) {
+        bf16 h, m, lo;
+        split3_bf16((e < 4 ? v0[e] : v1[e - 4]) / sz, h, m, lo);
+        ah[st][e] = h;
+        am[st][e] = m;
+        al[st][e] = lo;
+      }
     }
   }
 
@@ -88,7 +109,20 @@ __global__ void __launch_bounds__(256) icsa_compressed_logits_kernel(CompressedP
   };
   auto store_tile = [&](int buf) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) *reinterpret_cast<floatx4*>(&ks[buf][kc][kd + 4 * q]) = pre[q];
+    for (int half = 0; half < 2; ++half) {
+      bf16x8 h, m, lo;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        bf16 a, b, c;
+        split3_bf16(pre[2 * half + (e >> 2)][e & 3], a, b, c);
+        h[e] = a;
+        m[e] = b;
+        lo[e] = c;
+      }
+      *reinterpret_cast<bf16x8*>(&ks[buf][0][kc][kd + 8 * half]) = h;
+      *reinterpret_cast<bf16x8*>(&ks[buf][1][kc][kd + 8 * half]) = m;
+      *reinterpret_cast<bf16x8*>(&ks[buf][2][kc][kd + 8 * half]) = lo;
+    }
   };
 
   const float sq = sqrtf((float)ICSA_D);
@@ -102,10 +136,16 @@ __global__ void __launch_bounds__(256) icsa_compressed_logits_kernel(CompressedP
     if (more) load_tile(t + 1);
     floatx16 acc = {};
 #pragma unroll
-    for (int kk = 0; kk < 64; kk += 4) {
-      const floatx4 b = *reinterpret_cast<const floatx4*>(&ks[buf][li][64 * hl + kk]);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) acc = mfma32x32x2f32(a[kk + j], b[j], acc);
+    for (int st = 0; st < 8; ++st) {
+      const bf16x8 bh = *reinterpret_cast<const bf16x8*>(&ks[buf][0][li][16 * st + 8 * hl]);
+      const bf16x8 bm = *reinterpret_cast<const bf16x8*>(&ks[buf][1][li][16 * st + 8 * hl]);
+      const bf16x8 bl = *reinterpret_cast<const bf16x8*>(&ks[buf][2][li][16 * st + 8 * hl]);
+      acc = mfma32x32x16(al[st], bh, acc);
+      acc = mfma32x32x16(am[st], bm, acc);
+      acc = mfma32x32x16(ah[st], bl, acc);
+      acc = mfma32x32x16(am[st], bh, acc);
+      acc = mfma32x32x16(ah[st], bm, acc);
+      acc = mfma32x32x16(ah[st], bh, acc);
     }
     const int col = t * LG_COLS + li;
     if (col < NB) {
