@@ -38,9 +38,11 @@
 //   * !VROW: a V^T tile (128 d rows of 64 keys in kv_slot order) from the transposed copy
 //     the pipeline's pooling pass already writes for the flash kernel; PV operands are
 //     plain 16-byte reads, which the LDS delivers at a higher rate than transposing ones.
-// K(t+1) is issued as soon as
-// both waves finished reading K(t) and lands while the softmax and PV of tile t run;
-// V(t+1) is issued after PV(t) and lands during QK and softmax of tile t+1.  The epilogue fuses the residual and the scatter to [B, S, H, D].
+// K(t+1) is issued as soon as both waves finished reading K(t) and lands while the softmax
+// and PV of tile t run; V(t) is issued at the workgroup barrier that makes K(t) complete --
+// each wave reaches it only after its PV(t - 1) -- and lands during QK and softmax of tile
+// t, so a step needs three barriers.  The epilogue fuses the residual and the scatter to
+// [B, S, H, D].
 // The exact tiles are visited in ascending new-KV order starting at a block that advances
 // with the launch index (a rotation of the list), so that the workgroups resident on one
 // XCD sweep the new KV together.
@@ -323,13 +325,16 @@ icsa_sparse_kernel(SparseParams p) {
   float l_run = 0.f;
 
   int kv_pending = issue_k(0);
-  int vv_pending = issue_v(0);
+  int vv_pending = 0;
 
   // ---- 1. exact blocks ----
+  // Three barriers per block: V(t) is issued right after the first one, which every wave
+  // passes only after its PV(t - 1), so no barrier is needed after PV.
   for (int t = 0; t < T1; ++t) {
-    SP_WAIT_OLDER();                       // K(t); V(t) is the newer tile in flight
+    SP_WAIT_ALL();                         // K(t), the only load in flight
     fill_rows(kbuf, kv_pending);
-    ATT_BARRIER();
+    ATT_BARRIER();                         // K(t) complete; V buffer free
+    vv_pending = issue_v(t);
     qk();
     ATT_BARRIER();                       // K buffer free
     const int kv_next = issue_k(t + 1);    // T > T1: always a next K tile
@@ -369,10 +374,10 @@ icsa_sparse_kernel(SparseParams p) {
     fill_v(vv_pending);
     ATT_BARRIER();
     pv();
-    ATT_BARRIER();                       // V buffer free
-    vv_pending = issue_v(t + 1 < T1 ? t + 1 : T2);
     kv_pending = kv_next;
   }
+  ATT_BARRIER();                           // V buffer free
+  issue_v(T2);                             // pass 2's first V tile, after K(T1)
 
   // ---- 2a. interval pass 1: running max over the chunks ----
   float m_run = m_true;
@@ -394,11 +399,13 @@ icsa_sparse_kernel(SparseParams p) {
 
   // ---- 2b. interval pass 2: non-rescaled g terms, accumulated into o ----
   float m_c = m_true, gl_run = 0.f;
+  // Three barriers per chunk, as in the exact loop: V(g) is issued after the first one
+  // (V(T2) has been in its buffer since before pass 1).
   for (int ch = 0; ch < nc; ++ch) {
     const int g = T2 + ch;
-    if (ch == 0) SP_WAIT_ALL();            // K(T2) is the newest load
-    else SP_WAIT_OLDER();                  // V(g) is newer than K(g)
-    ATT_BARRIER();
+    SP_WAIT_ALL();                         // K(g); V(g - 1) was waited for before its PV
+    ATT_BARRIER();                         // K(g) complete; V buffer free
+    if (ch > 0) issue_v(g);
     qk();
     ATT_BARRIER();
     const bool more = g + 1 < T;
@@ -414,13 +421,12 @@ icsa_sparse_kernel(SparseParams p) {
         pf[2 * sub + (i >> 3)][i & 7] = (bf16)e;
       }
     gl_run += rs;
-    if (more) SP_WAIT_OLDER();
+    if (more) SP_WAIT_OLDER();             // V(g); K(g + 1) is the newer tile in flight
     else SP_WAIT_ALL();
     ATT_BARRIER();
     pv();
-    ATT_BARRIER();
-    if (more) issue_v(g + 1);
   }
+  ATT_BARRIER();                           // both waves' PV done before the staging below
 
   // ---- 3. combine + epilogue ----
   const float den = xhalf_sum(l_run) + 64.0f * xhalf_sum(gl_run);
