@@ -96,8 +96,10 @@ __global__ void __launch_bounds__(256) icsa_sparse_bwd_sums_kernel(SparseBwdPara
 // ------------------------------------------------------------------------------------------
 // Tile DMA.  A 16 KB row tile (64 rows x 128 dims, swizzled by rt_swz) is 16
 // LDS-DMA instructions, 8 per wave; each lands 1 KB at consecutive LDS addresses (lane l
-// at +16 l), so the XOR swizzle is applied on the global side.  Loads complete in issue
-// order: with the next step's tiles in flight a kernel waits with vmcnt(their count).
+// at +16 l), so the XOR swizzle is applied on the global side.  A step's tiles are the only
+// loads in flight when a kernel waits for them (vmcnt(0)): the next step's tiles are issued
+// after the workgroup barrier that follows, which also tells that both waves are done with
+// the buffer they overwrite (two buffers, one barrier per step).
 // ------------------------------------------------------------------------------------------
 #define BW_WAIT(n) asm volatile("s_waitcnt vmcnt(" #n ")" ::: "memory")
 
@@ -215,14 +217,9 @@ __global__ void __launch_bounds__(BW_THREADS) icsa_sparse_bwd_dq_kernel(SparseBw
   const float c64 = p.scale_log2 * (1.0f / 64.0f);
   issue(0);                                            // T >= nc >= 1
   for (int t = 0; t < T; ++t) {
-    const bool more = t + 1 < T;
-    if (more) {
-      issue(t + 1);                                    // the other buffer, free since step t - 1
-      BW_WAIT(16);                                     // step t's tiles
-    } else {
-      BW_WAIT(0);
-    }
-    ATT_BARRIER();
+    BW_WAIT(0);                                        // step t's tiles, the only loads in flight
+    ATT_BARRIER();                                     // step t complete; step t - 1's buffer read by both waves
+    if (t + 1 < T) issue(t + 1);                       // into that buffer
     const unsigned char* ks = smem_q + (t & 1) * 2 * K_TILE_BYTES;
     qk_tile_bw(s, reinterpret_cast<const bf16*>(ks), qf);                  // S^T[key][query]
     qk_tile_bw(dp, reinterpret_cast<const bf16*>(ks + K_TILE_BYTES), dof); // dP^T
@@ -248,7 +245,6 @@ __global__ void __launch_bounds__(BW_THREADS) icsa_sparse_bwd_dq_kernel(SparseBw
         }
     }
     pv_tile_tr<BW_PF, false>(dq, ks, tro, dsf);                      // dQ^T += K^T dS^T
-    ATT_BARRIER();                                     // buffer t & 1 consumed
   }
 
   // ---- epilogue: dq = scale * acc ----
@@ -362,16 +358,11 @@ __global__ void __launch_bounds__(BW_THREADS) icsa_sparse_bwd_dkv_kernel(SparseB
   bf16x8 pf[4], dsf[4];
   if (i_count > 0) issue(0);
   for (int n = 0; n < i_count; ++n) {
-    const bool more = n + 1 < i_count;
     bool on = key_valid;
     if (kInterval) on = on && ((wlist[n] >> (32 * wave + li)) & 1ull) == 0ull;
-    if (more) {
-      issue(n + 1);                                    // the other buffer, free since block n - 1
-      BW_WAIT(17);                                     // block n's tiles
-    } else {
-      BW_WAIT(0);
-    }
-    ATT_BARRIER();
+    BW_WAIT(0);                                        // block n's tiles, the only loads in flight
+    ATT_BARRIER();                                     // block n complete; block n - 1's buffer read by both waves
+    if (n + 1 < i_count) issue(n + 1);                 // into that buffer
     const unsigned char* qs = smem_dyn + (n & 1) * BWKV_BUF_BYTES;
     const unsigned char* dos = qs + K_TILE_BYTES;
     const float* lse_l = reinterpret_cast<const float*>(qs + 2 * K_TILE_BYTES);
@@ -435,7 +426,6 @@ __global__ void __launch_bounds__(BW_THREADS) icsa_sparse_bwd_dkv_kernel(SparseB
       if (t >= 32 && t < 48) elem(1, t - 32);
       __builtin_amdgcn_sched_barrier(0);
     }
-    ATT_BARRIER();                                     // buffer n & 1 consumed
   }
 
   __syncthreads();
