@@ -440,11 +440,26 @@ __device__ __forceinline__ int rank_idx(unsigned long long key) {
   return (int)(0xffffffffu - (uint32_t)(key & 0xffffffffull));
 }
 
+// Two workgroups per head (blockIdx.y): 0 ranks the source blocks and builds the new-KV
+// map, 1 ranks the query blocks by sharpness; the two rankings are independent.
 __global__ void __launch_bounds__(1024) icsa_select_kernel(SelectParams p) {
   __shared__ unsigned long long keys[ICSA_MAX_SORT];
   __shared__ int sel_l[ICSA_MAX_SORT];
   const int bh = blockIdx.x;
   const int NB = p.NB, n_t = p.n_t, n_s = p.n_s;
+  if (blockIdx.y == 1) {                       // uniform for the workgroup
+    if (!p.inject_order) {
+      int n2 = 1;
+      while (n2 < NB) n2 <<= 1;
+      for (int i = threadIdx.x; i < n2; i += blockDim.x)
+        keys[i] = i < NB ? rank_key(p.sharp[(int64_t)bh * NB + i], i) : 0ull;
+      __syncthreads();
+      bitonic_sort_desc(keys, n2);
+      for (int r = threadIdx.x; r < NB; r += blockDim.x)
+        p.order[(int64_t)bh * NB + r] = rank_idx(keys[r]);
+    }
+    return;
+  }
   int n1 = 1;
   while (n1 < n_s) n1 <<= 1;
   // column mass of source key blocks over target query blocks: the per-strip partial
@@ -473,16 +488,6 @@ __global__ void __launch_bounds__(1024) icsa_select_kernel(SelectParams p) {
     for (int r = threadIdx.x; r < p.topK; r += blockDim.x) sel_l[r] = p.sel[(int64_t)bh * p.topK + r];
   }
   __syncthreads();
-  if (!p.inject_order) {
-    int n2 = 1;
-    while (n2 < NB) n2 <<= 1;
-    for (int i = threadIdx.x; i < n2; i += blockDim.x)
-      keys[i] = i < NB ? rank_key(p.sharp[(int64_t)bh * NB + i], i) : 0ull;
-    __syncthreads();
-    bitonic_sort_desc(keys, n2);
-    for (int r = threadIdx.x; r < NB; r += blockDim.x)
-      p.order[(int64_t)bh * NB + r] = rank_idx(keys[r]);
-  }
   // new-KV block j -> source block: target blocks, then the selected source blocks in
   // ranked order, then zero padding (-1).
   for (int j = threadIdx.x; j < p.NKV; j += blockDim.x) {
@@ -497,7 +502,7 @@ __global__ void __launch_bounds__(1024) icsa_select_kernel(SelectParams p) {
 
 hipError_t launch_select(const SelectParams& p, hipStream_t stream) {
   if (p.n_s > ICSA_MAX_SORT || p.NB > ICSA_MAX_SORT) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(icsa_select_kernel, dim3(p.BH), dim3(1024), 0, stream, p);
+  hipLaunchKernelGGL(icsa_select_kernel, dim3(p.BH, 2), dim3(1024), 0, stream, p);
   return hipGetLastError();
 }
 
