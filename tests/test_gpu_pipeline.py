@@ -136,3 +136,16 @@ def test_degenerate_splits(gpu, flat, srr, real):
         assert z.n_diffuse == 0 and z.topK == 0
     else:
         assert z.n_peaked == 0 and z.topK > 0
+
+
+@pytest.mark.parametrize("where", ["t=0", "t=S"])
+def test_target_or_source_empty(gpu, where):
+    # t = 0: no target tokens, every V^T tile the attention kernels read comes from the
+    # selected source blocks (transposed after the selection); t = S: no source part, no
+    # selection, the new KV is the whole sequence
+    q, k, v, _ = make_inputs(H=2, real=512, pad=0, kind="random", seed=3)
+    S = q.shape[1]
+    t = 0 if where == "t=0" else S
+    _, _, info = _run_case(gpu, q, k, v, t)
+    z = info["sizes"]
+    assert (z.n_t, z.topK > 0) == ((0, True) if t == 0 else (z.NB, False))
