@@ -555,8 +555,8 @@ def main():
     # stage 1: the algorithmic bytes are read q, k, v + write the fp32 sums (the reference's
     # pooling, 2.076 GB at configuration 2); this pass also writes V^T of the target blocks
     # for the attention kernels (reported separately as pool_moved; the selected source
-    # blocks are transposed after the selection).  Stage 2: read sums, write P once, write
-    # out_c (the algorithmic minimum of the compressed stage).
+    # blocks are transposed after the selection).  Stage 2: read sums, write the NB x NB
+    # logits once, write out_c (the algorithmic minimum of the compressed stage).
     BH, NB = B * H, z["NB"]
     pool_bytes = 3 * B * S * H * D * 2 + 3 * BH * NB * D * 4
     pool_moved = pool_bytes + BH * D * (-(-t // 64) * 64) * 2

@@ -75,7 +75,8 @@ enum icsa_ws_slot {
                          only at target and selected source blocks                 */
   ICSA_WS_QB,         /* bf16 [B, S, H, D] copy of q (only when q is f32)           */
   ICSA_WS_KB,         /* bf16 [B, S, H, D] copy of k (only when k is f32)           */
-  ICSA_WS_P,          /* f32 [B*H, NB, NB]  compressed softmax P                    */
+  ICSA_WS_LOGITS,     /* f32 [B*H, NB, NB]  compressed logits L; the softmax P =
+                         exp(L - m) / z with ICSA_WS_RSTAT (P is not stored)        */
   ICSA_WS_OUTC,       /* f32 [B*H, NB, D]   compressed attention output             */
   ICSA_WS_SHARP,      /* f32 [B*H, NB]      sharpness                               */
   ICSA_WS_SRCSCORE,   /* f32 [B*H, n_s]     source-block column mass                */

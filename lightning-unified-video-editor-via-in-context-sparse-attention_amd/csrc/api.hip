@@ -92,7 +92,7 @@ Layout editing_layout(int B, int S, int H, const Sizes& z, int t, int q_dtype, i
   sz[ICSA_WS_VT] = BH * D * Sp * 2;
   sz[ICSA_WS_QB] = q_dtype == ICSA_F32 ? (int64_t)B * S * H * D * 2 : 0;
   sz[ICSA_WS_KB] = k_dtype == ICSA_F32 ? (int64_t)B * S * H * D * 2 : 0;
-  sz[ICSA_WS_P] = BH * z.NB * z.NB * 4;
+  sz[ICSA_WS_LOGITS] = BH * z.NB * z.NB * 4;
   sz[ICSA_WS_OUTC] = BH * z.NB * D * 4;
   sz[ICSA_WS_SHARP] = BH * z.NB * 4;
   sz[ICSA_WS_SRCSCORE] = BH * std::max(z.n_s, 1) * 4;
@@ -277,7 +277,7 @@ int editing_impl(ICSA_EDITING_ARGS, void* const* stage_events, const float* qsum
   // ---- stage 2: compressed attention, retrieval, split ----
   CompressedParams cp;
   cp.qsum = qsum; cp.ksum = ksum; cp.vsum = pp.sums[2];
-  cp.P = reinterpret_cast<float*>(WS(ICSA_WS_P));
+  cp.L = reinterpret_cast<float*>(WS(ICSA_WS_LOGITS));
   cp.out_c = reinterpret_cast<float*>(WS(ICSA_WS_OUTC));
   cp.sharp = reinterpret_cast<float*>(WS(ICSA_WS_SHARP));
   cp.colpart = reinterpret_cast<float*>(WS(ICSA_WS_COLP));

@@ -126,7 +126,7 @@ __global__ void __launch_bounds__(256) icsa_compressed_logits_kernel(CompressedP
   };
 
   const float sq = sqrtf((float)ICSA_D);
-  float* out = p.P + (int64_t)bh * NB * NB;
+  float* out = p.L + (int64_t)bh * NB * NB;
   load_tile(t0);
   store_tile(0);
   __syncthreads();
@@ -244,7 +244,7 @@ __global__ void __launch_bounds__(256) icsa_compressed_stats_kernel(CompressedPa
   const int64_t row = (int64_t)blockIdx.x * 4 + w;          // over BH * NB rows
   if (row >= (int64_t)p.BH * p.NB) return;
   const int NB = p.NB, n_t = p.n_t;
-  const float* L = p.P + row * NB;
+  const float* L = p.L + row * NB;
   float v[VPL];
   uint32_t key[VPL];                              // order keys of the target logits (0: none)
   float m = -INFINITY;
@@ -292,9 +292,10 @@ __global__ void __launch_bounds__(256) icsa_compressed_stats_kernel(CompressedPa
 
 // ---------------------------------------------------------------------------------------
 // (c) one 64-row strip of P per workgroup of 8 waves, in 64-column chunks: P = exp(L - m)/z
-//     written in place, out_c += P (Vs/size) with fp32 MFMA (wave w: rows 32 (w & 1),
-//     columns 32 (w >> 1)), and for strips holding target rows the column sums of the
-//     source columns over those rows (partials in strip order, summed by the select kernel).
+//     formed in LDS (nothing downstream reads P itself, so it is not written back),
+//     out_c += P (Vs/size) with fp32 MFMA (wave w: rows 32 (w & 1), columns 32 (w >> 1)), and
+//     for strips holding target rows the column sums of the source columns over those rows
+//     (partials in strip order, summed by the select kernel).
 // ---------------------------------------------------------------------------------------
 __global__ void __launch_bounds__(512) icsa_compressed_rows_kernel(CompressedParams p) {
   __shared__ float ps[64][68];
@@ -303,7 +304,7 @@ __global__ void __launch_bounds__(512) icsa_compressed_rows_kernel(CompressedPar
   const int strip = blockIdx.x, bh = blockIdx.y;
   const int NB = p.NB, n_t = p.n_t;
   const int r_base = strip * 64;
-  float* Pbh = p.P + (int64_t)bh * NB * NB;
+  const float* Lbh = p.L + (int64_t)bh * NB * NB;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   if (tid < 64) {
     const int row = r_base + tid;
@@ -326,7 +327,7 @@ __global__ void __launch_bounds__(512) icsa_compressed_rows_kernel(CompressedPar
     for (int x = 0; x < 8; ++x) {
       const int e = tid + 512 * x;
       const int row = r_base + (e >> 6), col = k0 + (e & 63);
-      lg[x] = (row < NB && col < NB) ? Pbh[(int64_t)row * NB + col] : 0.f;
+      lg[x] = (row < NB && col < NB) ? Lbh[(int64_t)row * NB + col] : 0.f;
     }
 #pragma unroll
     for (int x = 0; x < 4; ++x) {
@@ -340,15 +341,11 @@ __global__ void __launch_bounds__(512) icsa_compressed_rows_kernel(CompressedPar
   load_chunk(0);
   for (int k0 = 0; k0 < NB; k0 += 64) {
 #pragma unroll
-    for (int x = 0; x < 8; ++x) {                     // P = exp(L - m) / z, in place and to LDS
+    for (int x = 0; x < 8; ++x) {                     // P = exp(L - m) / z, to LDS only
       const int e = tid + 512 * x;
       const int r = e >> 6, kk = e & 63;
       const int row = r_base + r, col = k0 + kk;
-      float pv = 0.f;
-      if (row < NB && col < NB) {
-        pv = expf(lg[x] - row_m[r]) * row_iz[r];
-        Pbh[(int64_t)row * NB + col] = pv;
-      }
+      const float pv = (row < NB && col < NB) ? expf(lg[x] - row_m[r]) * row_iz[r] : 0.f;
       ps[r][kk] = pv;
     }
 #pragma unroll

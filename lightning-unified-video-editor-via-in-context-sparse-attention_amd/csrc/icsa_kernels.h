@@ -27,7 +27,7 @@ struct CompressedParams {
   const float* qsum;    // [BH, NB, D]
   const float* ksum;
   const float* vsum;
-  float* P;             // [BH, NB, NB] logits, then softmax probabilities in place
+  float* L;             // [BH, NB, NB] logits (P = exp(L - m) / z is formed where it is used)
   float* out_c;         // [BH, NB, D]
   float* sharp;         // [BH, NB]
   float* colpart;       // [BH, ceil(n_t/64), n_s] source-column sums per 64-row target strip

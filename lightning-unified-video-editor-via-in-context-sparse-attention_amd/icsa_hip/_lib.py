@@ -32,7 +32,7 @@ NOALLOC_SCRATCH_BYTES = 256 << 20
 STAGES = ["start", "pool", "compressed", "select", "sparse", "flash"]
 
 # workspace slots of icsa_editing_sparse_attention (enum icsa_ws_slot)
-WS_SLOTS = ["QSUM", "KSUM", "VSUM", "VT", "QB", "KB", "P", "OUTC", "SHARP", "SRCSCORE", "SEL",
+WS_SLOTS = ["QSUM", "KSUM", "VSUM", "VT", "QB", "KB", "LOGITS", "OUTC", "SHARP", "SRCSCORE", "SEL",
             "ORDER", "KVMAP", "KC32", "KC", "VCT", "L3", "KN", "VN", "VC", "NKSUM", "NVSUM",
             "COLP", "L3S", "RSTAT"]
 

@@ -165,12 +165,18 @@ def workspace_views(ws: torch.Tensor, offs, sizes: dict, B: int, H: int, D: int)
         return ws[off:off + nbytes].view(dtype).view(*shape)
 
     NB = z["NB"]
+    logits = view("LOGITS", torch.float32, (B, H, NB, NB))
+    row_stats = view("RSTAT", torch.float32, (B, H, NB, 2))      # row max m, 1 / row sum z
     return dict(
         sizes=z,
         q_sums=view("QSUM", torch.float32, (B, H, NB, D)),
         k_sums=view("KSUM", torch.float32, (B, H, NB, D)),
         v_sums=view("VSUM", torch.float32, (B, H, NB, D)),
-        P=view("P", torch.float32, (B, H, NB, NB)),
+        logits=logits,
+        row_stats=row_stats,
+        # the compressed softmax, formed from the stored logits and row statistics as the
+        # strip kernel forms it (the library does not store P)
+        P=torch.exp(logits - row_stats[..., :1]) * row_stats[..., 1:],
         out_c=view("OUTC", torch.float32, (B, H, NB, D)),
         sharpness=view("SHARP", torch.float32, (B, H, NB)),
         src_score=view("SRCSCORE", torch.float32, (B, H, max(z["n_s"], 1))),
