@@ -255,28 +255,11 @@ class WanSelfAttention(nn.Module):
         self.norm_k = WanRMSNorm(dim, eps=eps)
 
     capture = None    # a dict here receives the workspace views (decisions) of the next call
-    _qkv = None       # (key, weight, bias): q / k / v weights concatenated for one GEMM
-
-    def _qkv_weight(self):
-        """[3 dim, dim] weight and [3 dim] bias of q, k, v stacked, rebuilt whenever one of
-        the six parameters is replaced or modified in place (not part of the state dict)."""
-        params = (self.q.weight, self.k.weight, self.v.weight, self.q.bias, self.k.bias, self.v.bias)
-        key = tuple((p.data_ptr(), p._version, p.dtype, p.device) for p in params)
-        if self._qkv is None or self._qkv[0] != key:
-            with torch.no_grad():
-                w = torch.cat([p.detach() for p in params[:3]])
-                bias = torch.cat([p.detach() for p in params[3:]])
-            self._qkv = (key, w, bias)
-        return self._qkv[1], self._qkv[2]
 
     def forward(self, x, seq_lens, grid_sizes, source_video_grid_sizes, TAG, freqs):
         b, s = x.shape[:2]
-        # the three projections as one GEMM (x is read once); q / k / v are column slices of
-        # its output, which the producer and the attention call take with their strides
-        w, bias = self._qkv_weight()
-        yq, yk, yv = nn.functional.linear(x, w, bias).split(self.dim, dim=-1)
         res = wan_self_attention_core(
-            yq, yk, yv, self.alpha_1(x), self.norm_q.weight,
+            self.q(x), self.k(x), self.v(x), self.alpha_1(x), self.norm_q.weight,
             self.norm_k.weight, grid_sizes, source_video_grid_sizes, TAG, freqs,
             self.num_heads, self.eps, out_dtype=x.dtype, keep_workspace=self.capture is not None)
         if self.capture is not None:

@@ -133,24 +133,3 @@ def test_package_rope_table_matches_oracle():
     from icsa_hip import wan
     assert torch.allclose(wan.wan_freqs(128), W.wan_freqs(128), rtol=0, atol=1e-12)
 
-
-def test_stacked_qkv_weight_tracks_parameters():
-    # the self-attention's one-GEMM projection uses q, k, v stacked; the stack follows
-    # in-place updates and state-dict loads and stays out of the state dict
-    from icsa_hip.wan import WanSelfAttention
-    torch.manual_seed(0)
-    m = WanSelfAttention(64, 1)
-    w, b = m._qkv_weight()
-    assert torch.equal(w, torch.cat([m.q.weight, m.k.weight, m.v.weight]))
-    assert torch.equal(b, torch.cat([m.q.bias, m.k.bias, m.v.bias]))
-    assert m._qkv_weight()[0] is w                      # cached while nothing changes
-    with torch.no_grad():
-        m.k.weight.mul_(2.0)
-    w2, _ = m._qkv_weight()
-    assert w2 is not w and torch.equal(w2[64:128], m.k.weight)
-    sd = {n: torch.randn_like(t) for n, t in m.state_dict().items()}
-    m.load_state_dict(sd)
-    w3, b3 = m._qkv_weight()
-    assert torch.equal(w3, torch.cat([sd["q.weight"], sd["k.weight"], sd["v.weight"]]))
-    assert torch.equal(b3, torch.cat([sd["q.bias"], sd["k.bias"], sd["v.bias"]]))
-    assert not any("qkv" in n for n in m.state_dict())
