@@ -403,6 +403,8 @@ hipError_t launch_compressed(const CompressedParams& p, hipStream_t stream) {
     hipLaunchKernelGGL(icsa_compressed_stats_kernel<16>, sgrid, dim3(256), 0, stream, p);
   else if (p.NB <= 2048)
     hipLaunchKernelGGL(icsa_compressed_stats_kernel<32>, sgrid, dim3(256), 0, stream, p);
+  else if (p.NB <= 2560)                             // configuration 5: NB = 2363
+    hipLaunchKernelGGL(icsa_compressed_stats_kernel<40>, sgrid, dim3(256), 0, stream, p);
   else
     hipLaunchKernelGGL(icsa_compressed_stats_kernel<64>, sgrid, dim3(256), 0, stream, p);
   e = hipGetLastError();
