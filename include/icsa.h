@@ -71,8 +71,8 @@ enum icsa_ws_slot {
   ICSA_WS_QSUM = 0,   /* f32 [B*H, NB, D]   block sums of q                       */
   ICSA_WS_KSUM,       /* f32 [B*H, NB, D]                                          */
   ICSA_WS_VSUM,       /* f32 [B*H, NB, D]                                          */
-  ICSA_WS_VT,         /* bf16 [B*H, D, NB*64] V transposed (kv_slot order); written
-                         only at target and selected source blocks                 */
+  ICSA_WS_VT,         /* bf16 [B*H, D, (ceil(t/64) + topK)*64] V^T of the new KV
+                         (kv_slot order): target blocks, then the selected ones    */
   ICSA_WS_QB,         /* bf16 [B, S, H, D] copy of q (only when q is f32)           */
   ICSA_WS_KB,         /* bf16 [B, S, H, D] copy of k (only when k is f32)           */
   ICSA_WS_LOGITS,     /* f32 [B*H, NB, NB]  compressed logits L; the softmax P =

@@ -80,16 +80,19 @@ struct Layout {
   int64_t total;
 };
 
+// Columns of the pipeline's V^T: the new KV's tiles in order, the ceil(t / 64) target tiles
+// then the topK selected source blocks (tile j at columns 64 j .. 64 j + 63)
+int64_t vt_columns(const Sizes& z, int t) { return ((int64_t)ceil_div(t, ICSA_BLOCK) + z.topK) * ICSA_BLOCK; }
+
 Layout editing_layout(int B, int S, int H, const Sizes& z, int t, int q_dtype, int k_dtype) {
   const int64_t BH = (int64_t)B * H;
   const int64_t D = ICSA_D;
-  const int64_t Sp = (int64_t)z.NB * ICSA_BLOCK;
   const bool unaligned = (t % ICSA_BLOCK) != 0;
   int64_t sz[ICSA_WS_COUNT];
   sz[ICSA_WS_QSUM] = BH * z.NB * D * 4;
   sz[ICSA_WS_KSUM] = BH * z.NB * D * 4;
   sz[ICSA_WS_VSUM] = BH * z.NB * D * 4;
-  sz[ICSA_WS_VT] = BH * D * Sp * 2;
+  sz[ICSA_WS_VT] = BH * D * vt_columns(z, t) * 2;
   sz[ICSA_WS_QB] = q_dtype == ICSA_F32 ? (int64_t)B * S * H * D * 2 : 0;
   sz[ICSA_WS_KB] = k_dtype == ICSA_F32 ? (int64_t)B * S * H * D * 2 : 0;
   sz[ICSA_WS_LOGITS] = BH * z.NB * z.NB * 4;
@@ -234,7 +237,7 @@ int editing_impl(ICSA_EDITING_ARGS, void* const* stage_events, const float* qsum
   char* ws = reinterpret_cast<char*>(workspace);
   auto WS = [&](int slot) { return ws + L.off[slot]; };
   const int BH = B * H;
-  const int64_t Sp = (int64_t)z.NB * ICSA_BLOCK;
+  const int64_t Tvt = vt_columns(z, t_seq_len);
   const bool unaligned = (t_seq_len % ICSA_BLOCK) != 0;
 
   // ---- stage 1: pooling (+ V transposed, + bf16 copies of f32 q/k) ----
@@ -252,10 +255,10 @@ int editing_impl(ICSA_EDITING_ARGS, void* const* stage_events, const float* qsum
   pp.xb[1] = k_dtype == ICSA_F32 ? reinterpret_cast<bf16*>(WS(ICSA_WS_KB)) : nullptr;
   pp.xb_sb = (int64_t)S * H * ICSA_D; pp.xb_ss = (int64_t)H * ICSA_D; pp.xb_sh = ICSA_D;
   pp.vt = reinterpret_cast<bf16*>(WS(ICSA_WS_VT));
-  pp.vt_sb = (int64_t)H * ICSA_D * Sp; pp.vt_sh = ICSA_D * Sp; pp.vt_sd = Sp;
+  pp.vt_sb = (int64_t)H * ICSA_D * Tvt; pp.vt_sh = ICSA_D * Tvt; pp.vt_sd = Tvt;
   pp.vt_src = 2;
-  // V^T is read only at the target tiles and the selected source blocks: the pooling pass
-  // transposes the target blocks, the selected ones are transposed after the selection
+  // V^T holds the new KV's tiles only: the pooling pass transposes the target blocks (block
+  // n at columns 64 n ..), the selected source blocks follow after the selection
   pp.vt_limit = 1; pp.vt_nblk = ceil_div(t_seq_len, ICSA_BLOCK);
   pp.B = B; pp.S = S; pp.H = H; pp.NB = z.NB;
   ICSA_HIP_TRY(mark(ICSA_STAGE_START), "event");
@@ -304,7 +307,8 @@ int editing_impl(ICSA_EDITING_ARGS, void* const* stage_events, const float* qsum
   sp.inject_sel = inject_sel ? 1 : 0;
   sp.inject_order = inject_order ? 1 : 0;
   ICSA_HIP_TRY(launch_select(sp, stream), "select");
-  ICSA_HIP_TRY(launch_vt_blocks(pp, sel, z.n_t, std::max(z.topK, 1), z.topK, stream), "V^T of the selected blocks");
+  ICSA_HIP_TRY(launch_vt_blocks(pp, sel, z.n_t, std::max(z.topK, 1), z.topK, pp.vt_nblk, stream),
+               "V^T of the selected blocks");
 
   // ---- new-KV block sums (in place for aligned t, materialised otherwise) ----
   NewKvSumsParams np;

@@ -7,7 +7,8 @@
 // The new KV is never materialised: key tile j < n_tgt_tiles is target tile j of the
 // original sequence (keys >= t_limit masked: the partial last target tile), tile
 // n_tgt_tiles + r is source block sel_base + sel[r] (tokens >= Sk are zero keys with
-// logit 0, exactly like the reference's zero padding of k_padded).
+// logit 0, exactly like the reference's zero padding of k_padded).  K is read in place;
+// V^T holds tile j at columns 64 j .. 64 j + 63 (the pipeline writes it in that order).
 //
 // Workgroup = 8 waves = four 64-row query blocks (wave w: block w/2, rows 32*(w%2)..+31),
 // all sharing each K / V^T tile.  The waves form two groups, G0 = waves 0-3 and G1 = waves
@@ -188,7 +189,7 @@ icsa_flash_kernel(FlashParams p) {
       dma_dst = kbuf(j) + dw * 4096;
       dma_kvalid = k_valid;
     } else {
-      dma_rs = make_rsrc(vb + tok0, ((int64_t)(ICSA_D - 1) * p.vt_sd + ATT_BN) * 2);
+      dma_rs = make_rsrc(vb + (int64_t)j * ATT_BN, ((int64_t)(ICSA_D - 1) * p.vt_sd + ATT_BN) * 2);
       dma_dst = vbuf(j) + dw * 4096;
     }
   };

@@ -17,10 +17,11 @@ struct PoolParams {
   int B, S, H, NB;      // S tokens, NB = ceil(S / 64) blocks
 };
 hipError_t launch_pool(const PoolParams& p, hipStream_t stream);
-// V^T of a list of blocks only: block base + list[bh * stride + r], r < n, of x[vt_src]
-// (the selected source blocks, transposed after the selection)
+// V^T of a list of blocks only: block base + list[bh * stride + r], r < n, of x[vt_src],
+// stored as V^T block dst0 + r (the selected source blocks, transposed after the selection
+// into the columns that follow the target blocks)
 hipError_t launch_vt_blocks(const PoolParams& p, const int* list, int base, int stride, int n,
-                            hipStream_t stream);
+                            int dst0, hipStream_t stream);
 
 // ---------------------------------------------------------------- stage 2 (compressed.hip)
 struct CompressedParams {
@@ -88,7 +89,7 @@ hipError_t launch_gather(const GatherParams& p, hipStream_t stream);
 struct FlashParams {
   const bf16* q; int64_t q_sb, q_ss, q_sh;      // [B, Sq, H, D]
   const bf16* k; int64_t k_sb, k_ss, k_sh;      // [B, Sk, H, D]
-  const bf16* vt; int64_t vt_sb, vt_sh, vt_sd;  // [B, H, D, Skp]
+  const bf16* vt; int64_t vt_sb, vt_sh, vt_sd;  // [B, H, D, 64 n_tiles]: tile j at columns 64 j ..
   int B, H, Sq, Sk;
   const int* qblocks; int qb_offset, qb_stride; int n_qblk;   // per-bh q-block list
   int t_limit, n_tgt_tiles;        // KV tiles [0, n_tgt_tiles) of 64 keys, keys >= t_limit masked

@@ -162,10 +162,10 @@ hipError_t launch_pool(const PoolParams& p, hipStream_t stream) {
   return hipGetLastError();
 }
 
-// V^T of listed blocks: one workgroup per (b*h, list entry)
+// V^T of listed blocks: one workgroup per (b*h, list entry r), stored as V^T block dst0 + r
 template <typename T>
 __global__ void __launch_bounds__(256) icsa_vt_blocks_kernel(PoolParams p, const int* list, int base,
-                                                             int stride) {
+                                                             int stride, int dst0) {
   __shared__ bf16 vtile[ICSA_BLOCK][ICSA_D + 8];
   const int bh = blockIdx.x, r = blockIdx.y;
   const int b = bh / p.H, h = bh % p.H;
@@ -181,17 +181,17 @@ __global__ void __launch_bounds__(256) icsa_vt_blocks_kernel(PoolParams p, const
     *reinterpret_cast<bf16x8*>(&vtile[g + 16 * j][8 * c]) = pack8_bf16(v);
   }
   __syncthreads();
-  vt_store(p, n, b, h, vtile);
+  vt_store(p, dst0 + r, b, h, vtile);
 }
 
 hipError_t launch_vt_blocks(const PoolParams& p, const int* list, int base, int stride, int n,
-                            hipStream_t stream) {
+                            int dst0, hipStream_t stream) {
   if (n <= 0 || p.B * p.H == 0) return hipSuccess;
   if (!p.vt || !p.x[p.vt_src].p) return hipErrorInvalidValue;
   dim3 grid(p.B * p.H, n);
   if (p.x[p.vt_src].dtype == ICSA_DT_F32)
-    hipLaunchKernelGGL(icsa_vt_blocks_kernel<float>, grid, dim3(256), 0, stream, p, list, base, stride);
+    hipLaunchKernelGGL(icsa_vt_blocks_kernel<float>, grid, dim3(256), 0, stream, p, list, base, stride, dst0);
   else
-    hipLaunchKernelGGL(icsa_vt_blocks_kernel<bf16>, grid, dim3(256), 0, stream, p, list, base, stride);
+    hipLaunchKernelGGL(icsa_vt_blocks_kernel<bf16>, grid, dim3(256), 0, stream, p, list, base, stride, dst0);
   return hipGetLastError();
 }

@@ -35,9 +35,10 @@
 //   * VROW: 64 rows of the caller's row-major V, a row tile (attn_tile.h) whose PV
 //     operands are formed by transposing LDS reads -- no transposed copy of V is needed
 //     (the sparse host entry points, and the materialised new KV of t % 64 != 0);
-//   * !VROW: a V^T tile (128 d rows of 64 keys in kv_slot order) from the transposed copy
-//     the pipeline's pooling pass already writes for the flash kernel; PV operands are
-//     plain 16-byte reads, which the LDS delivers at a higher rate than transposing ones.
+//   * !VROW: a V^T tile (128 d rows of 64 keys in kv_slot order) from the pipeline's
+//     transposed copy of the new KV (new-KV block j at columns 64 j ..; written for the
+//     flash kernel by the pooling pass and after the selection); PV operands are plain
+//     16-byte reads, which the LDS delivers at a higher rate than transposing ones.
 // K(t+1) is issued as soon as both waves finished reading K(t) and lands while the softmax
 // and PV of tile t run; V(t) is issued at the workgroup barrier that makes K(t) complete --
 // each wave reaches it only after its PV(t - 1) -- and lands during QK and softmax of tile
@@ -74,6 +75,7 @@ icsa_sparse_kernel(SparseParams p) {
   __shared__ __attribute__((aligned(16))) unsigned char kbuf[SP_BUF_BYTES];
   __shared__ __attribute__((aligned(16))) unsigned char vbuf[SP_BUF_BYTES];
   __shared__ int src_l[SP_MAX_TOPK];                  // source block of exact tile t (-1: zeros)
+  __shared__ int nkv_l[SP_MAX_TOPK];                  // its new-KV block (V^T column block; -1: zeros)
   __shared__ unsigned long long sel_l[SP_MAX_CHUNKS];  // selected new-KV blocks per chunk
   __shared__ int rot_l;                               // exact tiles visited from list entry rot_l
 
@@ -114,6 +116,7 @@ icsa_sparse_kernel(SparseParams p) {
         if (j < sweep0) atomicAdd(&rot_l, 1);
       }
       src_l[t] = src;
+      nkv_l[t] = src >= 0 ? j : -1;
     }
   }
 
@@ -194,10 +197,11 @@ icsa_sparse_kernel(SparseParams p) {
         base = vbase + (src < 0 ? 0 : (int64_t)tok0 * p.v_st);
         bytes = valid > 0 ? ((int64_t)(valid - 1) * p.v_st + ICSA_D) * 2 : 0;
         rs2 = (int)p.v_st * 2;
-      } else {
-        valid = src < 0 ? 0 : ATT_BN;
-        base = vbase + (src < 0 ? 0 : tok0);
-        bytes = src < 0 ? 0 : ((int64_t)(ICSA_D - 1) * p.vt_sd + ATT_BN) * 2;
+      } else {                           // V^T holds new-KV block j at columns 64 j ..
+        const int jn = __builtin_amdgcn_readfirstlane(nkv_l[ex_entry(g)]);
+        valid = jn < 0 ? 0 : ATT_BN;
+        base = vbase + (jn < 0 ? 0 : (int64_t)jn * ATT_BN);
+        bytes = jn < 0 ? 0 : ((int64_t)(ICSA_D - 1) * p.vt_sd + ATT_BN) * 2;
         rs2 = (int)p.vt_sd * 2;
       }
     } else {
