@@ -226,11 +226,13 @@ int icsa_sparse_piecewise_attn_fwd(
 int64_t icsa_sparse_piecewise_attn_bwd_workspace_size(int B, int H, int TQ, int TKV, int D);
 
 /* Gradients of icsa_sparse_piecewise_attn_fwd: dout, q, out [B, H, TQ, D] and k, v
- * [B, H, TKV, D] bf16 (strides sb, sh, st), lse [B*H, TQ] and idx [B*H, TQ/64, top_k]
- * from the forward (distinct block indices per row; entries outside [0, TKV/64) are
- * skipped).  dq / dk / dv are written (not accumulated) as bf16 or f32 (dtype codes).
- * Deterministic: every gradient is a fixed-order sum, no atomics.  TQ and TKV must be
- * multiples of 64 (ICSA_EINVAL otherwise; the forward also takes ragged lengths). */
+ * [B, H, TKV, D] bf16 (strides sb, sh, st), lse [B*H, TQ] and idx [B*H, cdiv(TQ, 64),
+ * top_k] from the forward (distinct block indices per row; entries outside
+ * [0, cdiv(TKV, 64)) are skipped).  dq / dk / dv are written (not accumulated) as bf16 or
+ * f32 (dtype codes).  Deterministic: every gradient is a fixed-order sum, no atomics.
+ * Ragged TQ / TKV as the Triton backward (triton_kernels.py:265-486, :541-598): rows past
+ * the lengths read as zero, keys past TKV take no part in the exact blocks, the last
+ * block's sums cover its real rows. */
 int icsa_sparse_piecewise_attn_bwd(
     const void* dout, int64_t do_sb, int64_t do_sh, int64_t do_st,
     const void* q, int64_t q_sb, int64_t q_sh, int64_t q_st,

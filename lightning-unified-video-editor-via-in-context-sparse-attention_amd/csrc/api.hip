@@ -783,7 +783,7 @@ struct BwLayout {
 // in LDS).
 BwLayout bwd_layout(int B, int H, int TQ, int TKV) {
   const int64_t BH = (int64_t)B * H;
-  const int NQ = TQ / ICSA_BLOCK, NKV = TKV / ICSA_BLOCK;
+  const int NQ = ceil_div(TQ, ICSA_BLOCK), NKV = ceil_div(TKV, ICSA_BLOCK);
   const int nc = ceil_div(NKV, 64), NKVp = nc * 64;
   BwLayout L;
   const int want = std::max(1, ceil_div(1024, (int)std::max<int64_t>(1, BH * nc)));
@@ -794,7 +794,7 @@ BwLayout bwd_layout(int B, int H, int TQ, int TKV) {
   int64_t o = 0;
   L.ksum = o; o += align256(BH * NKV * ICSA_D * 4);
   L.vsum = o; o += align256(BH * NKV * ICSA_D * 4);
-  L.dvec = o; o += align256(BH * (int64_t)TQ * 4);
+  L.dvec = o; o += align256(BH * (int64_t)NQ * ICSA_BLOCK * 4);   // D rows padded to whole blocks
   L.selbits = o; o += align256(BH * NQ * (int64_t)nc * 8);
   L.kcb = o; o += align256(BH * NKVp * ICSA_D * 2);
   L.vcb = o; o += align256(BH * NKVp * ICSA_D * 2);
@@ -809,7 +809,6 @@ extern "C" {
 
 int64_t icsa_sparse_piecewise_attn_bwd_workspace_size(int B, int H, int TQ, int TKV, int D) {
   if (B <= 0 || H <= 0 || TQ <= 0 || TKV <= 0 || D != ICSA_D) return ICSA_EINVAL;
-  if (TQ % ICSA_BLOCK || TKV % ICSA_BLOCK) return ICSA_EINVAL;
   return bwd_layout(B, H, TQ, TKV).total;
 }
 
@@ -830,8 +829,6 @@ int icsa_sparse_piecewise_attn_bwd(
   if ((rc = check_dtype(dq_dtype, "dq")) || (rc = check_dtype(dk_dtype, "dk")) || (rc = check_dtype(dv_dtype, "dv")))
     return rc;
   if (TKV <= 0) return fail(ICSA_EINVAL, "TKV must be positive");
-  if (TQ % ICSA_BLOCK || TKV % ICSA_BLOCK)
-    return fail(ICSA_EINVAL, "TQ/TKV must be divisible by the block size 64 (got %d, %d)", TQ, TKV);
   if (!dout || !q || !k || !v || !out || !lse || !idx || !dq || !dk || !dv || !workspace)
     return fail(ICSA_EINVAL, "null pointer argument");
   if (!row_ok(dout, ICSA_BF16, do_sb, do_sh, do_st) || !row_ok(q, ICSA_BF16, q_sb, q_sh, q_st) ||
@@ -839,7 +836,7 @@ int icsa_sparse_piecewise_attn_bwd(
       !row_ok(out, ICSA_BF16, o_sb, o_sh, o_st) || !row_ok(dq, dq_dtype, dq_sb, dq_sh, dq_st) ||
       !row_ok(dk, dk_dtype, dk_sb, dk_sh, dk_st) || !row_ok(dv, dv_dtype, dv_sb, dv_sh, dv_st))
     return fail(ICSA_EINVAL, "rows must be 16-byte aligned (pointer and strides)");
-  const int NQ = TQ / ICSA_BLOCK, NKV = TKV / ICSA_BLOCK;
+  const int NQ = ceil_div(TQ, ICSA_BLOCK), NKV = ceil_div(TKV, ICSA_BLOCK);   // ragged: last block partial
   if (NQ > 4096 || NKV > 2048)
     return fail(ICSA_EUNSUPPORTED, "NQ=%d / NKV=%d exceed limits (4096 / 2048)", NQ, NKV);
   if (top_k < 1 || top_k > 512 || top_k > NKV)

@@ -24,6 +24,10 @@
 //   dk / dv kernel, the roles swapped: S = Q K^T and dP = dO V^T with the Q / dO rows in
 //     LDS and K, V of the wave's 32 keys in registers; dV^T += dO^T P and dK^T += Q^T dS
 //     with the transposed Q / dO tiles in LDS.
+// Ragged lengths (the Triton host): NQ = cdiv(TQ, 64), NKV = cdiv(TKV, 64).  Rows past TQ
+// and TKV read as zero (q, dO, lse, D, k, v: the tensor descriptors' zero fill), keys past
+// TKV are masked out of the exact part (triton_kernels.py:348), and gradient rows past TQ /
+// TKV are not stored.
 // P and dS are rounded to bf16 for the MFMA (the reference rounds P for dv and uses fp32
 // dots for dq / dk).  Workgroup = 2 waves; wave w owns queries (or keys) 32 w .. 32 w + 31.
 #include "attn_tile.h"
@@ -52,9 +56,10 @@ __global__ void __launch_bounds__(256) icsa_sparse_bwd_rows_kernel(SparseBwdPara
   }
   const int r = t >> 2, qq = t & 3;               // row, quarter of D (32 elements)
   const int tok = i * ICSA_BLOCK + r;
+  float acc = 0.f;
+  if (tok < p.TQ) {                               // rows past TQ: D = 0
   const bf16* dor = p.dout + (int64_t)b * p.do_sb + (int64_t)h * p.do_sh + (int64_t)tok * p.do_st + 32 * qq;
   const bf16* orr = p.out + (int64_t)b * p.o_sb + (int64_t)h * p.o_sh + (int64_t)tok * p.o_st + 32 * qq;
-  float acc = 0.f;
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
     const bf16x8 a = *reinterpret_cast<const bf16x8*>(dor + 8 * c);
@@ -62,9 +67,10 @@ __global__ void __launch_bounds__(256) icsa_sparse_bwd_rows_kernel(SparseBwdPara
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc = fmaf((float)a[e], (float)o[e], acc);
   }
+  }
   acc += __shfl_xor(acc, 1, 64);
   acc += __shfl_xor(acc, 2, 64);
-  if (qq == 0) p.dvec[(int64_t)bh * p.TQ + tok] = acc;
+  if (qq == 0) p.dvec[(int64_t)bh * p.NQ * ICSA_BLOCK + tok] = acc;   // D rows padded to NQ * 64
   __syncthreads();
   if (t < p.nc) p.selbits[((int64_t)bh * p.NQ + i) * p.nc + t] = sel[t];
 }
@@ -131,15 +137,28 @@ __device__ __forceinline__ void qk_tile_bw(floatx16 s[2], const bf16* tile, cons
   s[1] = acc1;
 }
 
+// Rows >= valid lie outside the buffer range and land nothing: bw_fill_rows zeroes them once
+// the tile's loads have completed.
 __device__ __forceinline__ void bw_dma_rows(unsigned char* tile, const bf16* base, int64_t rs, int wave,
-                                            int lane) {
-  const __amdgpu_buffer_rsrc_t rsrc = make_rsrc(base, ((int64_t)(ICSA_BLOCK - 1) * rs + ICSA_D) * 2);
+                                            int lane, int valid = ICSA_BLOCK) {
+  const __amdgpu_buffer_rsrc_t rsrc =
+      make_rsrc(base, valid > 0 ? ((int64_t)(valid - 1) * rs + ICSA_D) * 2 : 0);
   unsigned char* dst = tile + wave * 8192;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int r = 32 * wave + 4 * i + (lane >> 4);
     const int off = (int)(r * rs * 2) + (((lane & 15) ^ rt_swz(r)) << 4);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_ptr)(dst + 1024 * i), 16, off, 0, 0, 0);
+  }
+}
+
+// Zero this wave's rows >= valid of a row tile (the bytes its DMA lanes would have landed).
+__device__ __forceinline__ void bw_fill_rows(unsigned char* tile, int valid, int wave, int lane) {
+  if (valid >= ICSA_BLOCK) return;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int r = 32 * wave + 4 * i + (lane >> 4);
+    if (r >= valid) *reinterpret_cast<u32x4*>(tile + r * ICSA_D * 2 + (lane & 15) * 16) = u32x4{0u, 0u, 0u, 0u};
   }
 }
 
@@ -182,11 +201,13 @@ __global__ void __launch_bounds__(BW_THREADS) icsa_sparse_bwd_dq_kernel(SparseBw
     }
     if (lane == 0) *n_ex_l = cnt;
   }
+  const int q_valid = max(0, min(32, p.TQ - qtok0));  // this wave's real query rows
   bf16x8 qf[8], dof[8];
-  load_q_frags(qf, p.q + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh + (int64_t)qtok0 * p.q_st, p.q_st, 32);
-  load_q_frags(dof, p.dout + (int64_t)b * p.do_sb + (int64_t)h * p.do_sh + (int64_t)qtok0 * p.do_st, p.do_st, 32);
-  const float lse = p.lse[(int64_t)bh * p.TQ + qtok0 + li];
-  const float dd = p.dvec[(int64_t)bh * p.TQ + qtok0 + li];
+  load_q_frags(qf, p.q + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh + (int64_t)qtok0 * p.q_st, p.q_st, q_valid);
+  load_q_frags(dof, p.dout + (int64_t)b * p.do_sb + (int64_t)h * p.do_sh + (int64_t)qtok0 * p.do_st, p.do_st,
+               q_valid);
+  const float lse = li < q_valid ? p.lse[(int64_t)bh * p.TQ + qtok0 + li] : 0.f;
+  const float dd = p.dvec[(int64_t)bh * p.NQ * ICSA_BLOCK + qtok0 + li];
   int tro[4];
   rt_tr_offsets<false>(tro, lane);
   __syncthreads();
@@ -197,13 +218,18 @@ __global__ void __launch_bounds__(BW_THREADS) icsa_sparse_bwd_dq_kernel(SparseBw
   const bf16* vb = p.v + (int64_t)b * p.v_sb + (int64_t)h * p.v_sh;
   const bf16* kcb = p.kcb + (int64_t)bh * p.NKVp * ICSA_D;
   const bf16* vcb = p.vcb + (int64_t)bh * p.NKVp * ICSA_D;
+  // real key rows of exact step t (the last block of a ragged TKV is partial)
+  auto key_rows = [&](int t) -> int {
+    return min(ICSA_BLOCK, p.TKV - __builtin_amdgcn_readfirstlane(src_l[t]) * ICSA_BLOCK);
+  };
   // buffer u: K rows at 2 u tiles, V rows at 2 u + 1
   auto issue = [&](int t) {
     unsigned char* kt = smem_q + (t & 1) * 2 * K_TILE_BYTES;
     if (t < n_ex) {
       const int j = __builtin_amdgcn_readfirstlane(src_l[t]);
-      bw_dma_rows(kt, kb + (int64_t)j * ICSA_BLOCK * p.k_st, p.k_st, wave, lane);
-      bw_dma_rows(kt + K_TILE_BYTES, vb + (int64_t)j * ICSA_BLOCK * p.v_st, p.v_st, wave, lane);
+      const int valid = key_rows(t);
+      bw_dma_rows(kt, kb + (int64_t)j * ICSA_BLOCK * p.k_st, p.k_st, wave, lane, valid);
+      bw_dma_rows(kt + K_TILE_BYTES, vb + (int64_t)j * ICSA_BLOCK * p.v_st, p.v_st, wave, lane, valid);
     } else {
       const int ch = t - n_ex;
       bw_dma_rows(kt, kcb + (int64_t)ch * ICSA_BLOCK * ICSA_D, ICSA_D, wave, lane);
@@ -217,7 +243,12 @@ __global__ void __launch_bounds__(BW_THREADS) icsa_sparse_bwd_dq_kernel(SparseBw
   const float c64 = p.scale_log2 * (1.0f / 64.0f);
   issue(0);                                            // T >= nc >= 1
   for (int t = 0; t < T; ++t) {
+    const int kvalid = t < n_ex ? key_rows(t) : ICSA_BLOCK;
     BW_WAIT(0);                                        // step t's tiles, the only loads in flight
+    if (kvalid < ICSA_BLOCK) {                         // zero key / value rows past TKV
+      bw_fill_rows(smem_q + (t & 1) * 2 * K_TILE_BYTES, kvalid, wave, lane);
+      bw_fill_rows(smem_q + (t & 1) * 2 * K_TILE_BYTES + K_TILE_BYTES, kvalid, wave, lane);
+    }
     ATT_BARRIER();                                     // step t complete; step t - 1's buffer read by both waves
     if (t + 1 < T) issue(t + 1);                       // into that buffer
     const unsigned char* ks = smem_q + (t & 1) * 2 * K_TILE_BYTES;
@@ -228,7 +259,8 @@ __global__ void __launch_bounds__(BW_THREADS) icsa_sparse_bwd_dq_kernel(SparseBw
       for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
-          const float pr = __builtin_amdgcn_exp2f(fmaf(s[sub][e], p.scale_log2, -lse));
+          const bool masked = 32 * sub + acc_row(e, lane) >= kvalid;   // keys past TKV
+          const float pr = masked ? 0.f : __builtin_amdgcn_exp2f(fmaf(s[sub][e], p.scale_log2, -lse));
           dsf[2 * sub + (e >> 3)][e & 7] = (bf16)(pr * (dp[sub][e] - dd));
         }
     } else {                                           // unselected block sums: score / 64, dS / 64
@@ -254,7 +286,7 @@ __global__ void __launch_bounds__(BW_THREADS) icsa_sparse_bwd_dq_kernel(SparseBw
   __syncthreads();
   AlphaView none;
   none.p = nullptr; none.scalar = 0.f; none.sb = none.ss = none.sh = none.sd = 0; none.dtype = ICSA_DT_F32;
-  store_rows(o_lds, p.dq, b, h, qtok0, 32, nullptr, none);
+  store_rows(o_lds, p.dq, b, h, qtok0, q_valid, nullptr, none);
 }
 
 // ------------------------------------------------------------------------------------------
@@ -300,9 +332,10 @@ __global__ void __launch_bounds__(BW_THREADS) icsa_sparse_bwd_dkv_kernel(SparseB
   if (kInterval) {
     load_q_frags(kf, p.kcb + ((int64_t)bh * p.NKVp + key0) * ICSA_D, ICSA_D, 32);
     load_q_frags(vf, p.vcb + ((int64_t)bh * p.NKVp + key0) * ICSA_D, ICSA_D, 32);
-  } else {
-    load_q_frags(kf, p.k + (int64_t)b * p.k_sb + (int64_t)h * p.k_sh + (int64_t)key0 * p.k_st, p.k_st, 32);
-    load_q_frags(vf, p.v + (int64_t)b * p.v_sb + (int64_t)h * p.v_sh + (int64_t)key0 * p.v_st, p.v_st, 32);
+  } else {                                             // keys past TKV read as zero
+    const int kv = max(0, min(32, p.TKV - key0));
+    load_q_frags(kf, p.k + (int64_t)b * p.k_sb + (int64_t)h * p.k_sh + (int64_t)key0 * p.k_st, p.k_st, kv);
+    load_q_frags(vf, p.v + (int64_t)b * p.v_sb + (int64_t)h * p.v_sh + (int64_t)key0 * p.v_st, p.v_st, kv);
   }
   int tro[4];
   rt_tr_offsets<false>(tro, lane);
@@ -333,22 +366,26 @@ __global__ void __launch_bounds__(BW_THREADS) icsa_sparse_bwd_dkv_kernel(SparseB
     i_count = *qcount;
   }
 
-  const int ckey = key0 + li;                          // interval: this lane's compressed block
-  const bool key_valid = !kInterval || ckey < p.NKV;
+  const int ckey = key0 + li;                          // this lane's key (interval: compressed block)
+  const bool key_valid = ckey < (kInterval ? p.NKV : p.TKV);
   const float cexp = kInterval ? p.scale_log2 * (1.0f / 64.0f) : p.scale_log2;
   const float dmul = kInterval ? 64.0f : 1.0f;
   const float dsmul = kInterval ? (1.0f / 64.0f) : 1.0f;
 
   const bf16* qb0 = p.q + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh;
   const bf16* dob0 = p.dout + (int64_t)b * p.do_sb + (int64_t)h * p.do_sh;
-  const float* rowvec = (wave == 0 ? p.lse : p.dvec) + (int64_t)bh * p.TQ;
-  auto qblock = [&](int n) -> int { return kInterval ? i_begin + n : (int)qlist[n]; };
+  const float* rowvec = wave == 0 ? p.lse + (int64_t)bh * p.TQ : p.dvec + (int64_t)bh * p.NQ * ICSA_BLOCK;
+  auto qblock = [&](int n) -> int {
+    return kInterval ? i_begin + n : __builtin_amdgcn_readfirstlane((int)qlist[n]);
+  };
+  // real query rows of block qblock(n) (the last block of a ragged TQ is partial)
+  auto q_rows = [&](int n) -> int { return min(ICSA_BLOCK, p.TQ - qblock(n) * ICSA_BLOCK); };
   auto issue = [&](int n) {
-    const int i = qblock(n);
+    const int i = qblock(n), valid = q_rows(n);
     unsigned char* buf = smem_dyn + (n & 1) * BWKV_BUF_BYTES;
-    bw_dma_rows(buf, qb0 + (int64_t)i * ICSA_BLOCK * p.q_st, p.q_st, wave, lane);
-    bw_dma_rows(buf + K_TILE_BYTES, dob0 + (int64_t)i * ICSA_BLOCK * p.do_st, p.do_st, wave, lane);
-    const __amdgpu_buffer_rsrc_t rr = make_rsrc(rowvec + (int64_t)i * ICSA_BLOCK, ICSA_BLOCK * 4);
+    bw_dma_rows(buf, qb0 + (int64_t)i * ICSA_BLOCK * p.q_st, p.q_st, wave, lane, valid);
+    bw_dma_rows(buf + K_TILE_BYTES, dob0 + (int64_t)i * ICSA_BLOCK * p.do_st, p.do_st, wave, lane, valid);
+    const __amdgpu_buffer_rsrc_t rr = make_rsrc(rowvec + (int64_t)i * ICSA_BLOCK, valid * 4);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rr, (lds_ptr)(buf + 2 * K_TILE_BYTES + wave * 256), 4,
                                              lane * 4, 0, 0, 0);
   };
@@ -361,6 +398,13 @@ __global__ void __launch_bounds__(BW_THREADS) icsa_sparse_bwd_dkv_kernel(SparseB
     bool on = key_valid;
     if (kInterval) on = on && ((wlist[n] >> (32 * wave + li)) & 1ull) == 0ull;
     BW_WAIT(0);                                        // block n's tiles, the only loads in flight
+    const int qvalid = q_rows(n);
+    if (qvalid < ICSA_BLOCK) {                         // zero Q / dO rows and lse / D past TQ
+      unsigned char* buf = smem_dyn + (n & 1) * BWKV_BUF_BYTES;
+      bw_fill_rows(buf, qvalid, wave, lane);
+      bw_fill_rows(buf + K_TILE_BYTES, qvalid, wave, lane);
+      if (lane >= qvalid) reinterpret_cast<float*>(buf + 2 * K_TILE_BYTES + wave * 256)[lane] = 0.f;
+    }
     ATT_BARRIER();                                     // block n complete; block n - 1's buffer read by both waves
     if (n + 1 < i_count) issue(n + 1);                 // into that buffer
     const unsigned char* qs = smem_dyn + (n & 1) * BWKV_BUF_BYTES;
@@ -455,13 +499,14 @@ __global__ void __launch_bounds__(BW_THREADS) icsa_sparse_bwd_dkv_kernel(SparseB
       ivec[d] = sk * p.scale;
       ivec[ICSA_D + d] = sv;
     }
+    const int kv = max(0, min(32, p.TKV - key0));     // rows past TKV are not stored
     stage_o(o_lds, dk, p.scale);
     __syncthreads();
-    store_rows(o_lds, p.dk, b, h, key0, 32, ivec, one);
+    store_rows(o_lds, p.dk, b, h, key0, kv, ivec, one);
     __syncthreads();
     stage_o(o_lds, dv, 1.f);
     __syncthreads();
-    store_rows(o_lds, p.dv, b, h, key0, 32, ivec + ICSA_D, one);
+    store_rows(o_lds, p.dv, b, h, key0, kv, ivec + ICSA_D, one);
   }
 }
 

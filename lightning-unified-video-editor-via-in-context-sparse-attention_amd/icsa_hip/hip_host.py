@@ -219,15 +219,16 @@ def sparse_piecewise_attn_1st_intervals_bwd_hip(do, q, k, v, out, lse, indices, 
     SparsePiecewiseAttn1stIntervalsFunction.backward (triton_kernels.py:541-598) computes
     them from the saved (q, k, v, out, lse, indices), without atomics (the same inputs give
     the same bits).  ``grad_dtype``: bf16 (default: q.dtype, as the reference's final cast)
-    or float32.  ``indices`` must hold distinct blocks in ``[0, TKV/64)`` per query block
+    or float32.  ``indices`` must hold distinct blocks in ``[0, cdiv(TKV, 64))`` per query block
     (the forward's top-k always does; the reference's atomics would count a repeated entry
     twice in every gradient, this build's key-major dk / dv pass once), which
-    ``check_indices`` verifies on the host (one device sync).  TQ and TKV must be multiples
-    of 64 here (the forward also takes ragged lengths)."""
-    _check_sparse_args(q, k, v, 64)
+    ``check_indices`` verifies on the host (one device sync).  Ragged TQ / TKV as the
+    reference's Triton backward: ``cdiv`` blocks, rows past the lengths read as zero and keys
+    past TKV masked out of the exact blocks (triton_kernels.py:348, :404)."""
+    _check_sparse_args(q, k, v, 64, aligned=False)
     B, H, TQ, D = q.shape
     TKV = k.shape[2]
-    NQ = TQ // BLOCK_M
+    NQ = -(-TQ // BLOCK_M)
     _require(do.shape == q.shape and out.shape == q.shape, "do / out must be [B, H, TQ, D] like q")
     _require(do.dtype == torch.bfloat16 and out.dtype == torch.bfloat16, "do / out must be bfloat16")
     _require(all(t.device == q.device for t in (k, v, do, out, lse, indices)),
@@ -242,7 +243,7 @@ def sparse_piecewise_attn_1st_intervals_bwd_hip(do, q, k, v, out, lse, indices, 
     idx = indices.to(dtype=torch.int32).contiguous()
     top_k = idx.shape[-1]
     if check_indices:
-        check_index_lists(idx, TKV // BLOCK_M, "indices")
+        check_index_lists(idx, -(-TKV // BLOCK_M), "indices")
     L = _lib.lib()
     dq = torch.empty(B, H, TQ, D, dtype=gd, device=q.device)
     dk = torch.empty(B, H, TKV, D, dtype=gd, device=q.device)

@@ -16,6 +16,13 @@ Restated from the reference (paths relative to the reference repository root):
 * ``triton_kernels.py:541-598``  ``SparsePiecewiseAttn1stIntervalsFunction.backward``: fp32
   gradients, cast to the inputs' dtype at the end.
 
+Ragged lengths (the Triton host passes any TQ / TKV): ``NQ = cdiv(TQ, 64)``,
+``NKV = cdiv(TKV, 64)``; q / dO / o rows past TQ and k / v rows past TKV are zero (the
+reference's tensor descriptors read zeros there, lse included, :284-313), keys at
+positions >= TKV are masked out of the exact part (``-inf``, :348), the interval takes
+every unselected block ``c < NKV`` with the block sums over the real rows and the same
+``/ 64`` and weight 64 (:400-412), and only rows < TQ / < TKV of the gradients exist.
+
 The reference's fp32 atomics become plain sums here (the order of a float64 sum does not
 matter at the tolerance).  The lse passed in is used as given: the forward's
 non-rescaled interval accumulators make it differ from the true log-sum-exp when the
@@ -45,17 +52,21 @@ def sparse_piecewise_attn_bwd(do: torch.Tensor, q: torch.Tensor, k: torch.Tensor
                               indices: torch.Tensor, dtype=torch.float64):
     """Gradients ``(dq, dk, dv)`` (``dtype``) of the sparse piecewise attention.
 
-    q, do, o ``[B,H,TQ,D]``; k, v ``[B,H,TKV,D]`` (TQ, TKV multiples of 64); lse ``[B,H,TQ]``
+    q, do, o ``[B,H,TQ,D]``; k, v ``[B,H,TKV,D]`` (any lengths); lse ``[B,H,TQ]``
     in log2 units; indices ``[B,H,NQ,top_k]`` (selected key blocks per query block, in any
     order, distinct)."""
-    B, H, TQ, D = q.shape
-    TKV = k.shape[2]
-    assert TQ % BLOCK_M == 0 and TKV % BLOCK_M == 0
-    NQ, NKV = TQ // BLOCK_M, TKV // BLOCK_M
+    B, H, TQ0, D = q.shape
+    TKV0 = k.shape[2]
+    NQ, NKV = -(-TQ0 // BLOCK_M), -(-TKV0 // BLOCK_M)
+    TQ, TKV = NQ * BLOCK_M, NKV * BLOCK_M
     top_k = indices.shape[-1]
     scale = 1.0 / math.sqrt(D)
-    qd, kd, vd, dod, od = (t.to(dtype) for t in (q, k, v, do, o))
-    lse_n = lse.to(dtype) / LOG2E                          # natural-log units
+    pad_q = lambda t: torch.nn.functional.pad(t.to(dtype), (0, 0, 0, TQ - TQ0))
+    pad_k = lambda t: torch.nn.functional.pad(t.to(dtype), (0, 0, 0, TKV - TKV0))
+    qd, dod, od = pad_q(q), pad_q(do), pad_q(o)
+    kd, vd = pad_k(k), pad_k(v)
+    lse_n = torch.nn.functional.pad(lse.to(dtype), (0, TQ - TQ0)) / LOG2E   # natural-log units
+    key_real = (torch.arange(TKV) < TKV0).view(NKV, BLOCK_M)              # exact-part key mask
     Dv = (dod * od).sum(-1)                                # [B,H,TQ]
     KC = kd.view(B, H, NKV, BLOCK_M, D).sum(3)
     VC = vd.view(B, H, NKV, BLOCK_M, D).sum(3)
@@ -73,6 +84,7 @@ def sparse_piecewise_attn_bwd(do: torch.Tensor, q: torch.Tensor, k: torch.Tensor
     lb = lse_n.view(B, H, NQ, BLOCK_M, 1)
     Db = Dv.view(B, H, NQ, BLOCK_M, 1)
     p = torch.exp(torch.matmul(qb, kx.transpose(-2, -1)) * scale - lb)
+    p = p * key_real[idx].reshape(B, H, NQ, 1, top_k * BLOCK_M)
     ds = p * (torch.matmul(dob, vx.transpose(-2, -1)) - Db)
     dq = torch.matmul(ds, kx) * scale
     dkx = (torch.matmul(ds.transpose(-2, -1), qb) * scale).view(B, H, NQ, top_k, BLOCK_M, D)
@@ -97,4 +109,5 @@ def sparse_piecewise_attn_bwd(do: torch.Tensor, q: torch.Tensor, k: torch.Tensor
     dVC = torch.matmul(pc.transpose(-2, -1), dod)
     dk = dk + (dKC / BLOCK_M)[:, :, :, None, :]
     dv = dv + dVC[:, :, :, None, :]
-    return dq, dk.reshape(B, H, TKV, D), dv.reshape(B, H, TKV, D)
+    return (dq[:, :, :TQ0], dk.reshape(B, H, TKV, D)[:, :, :TKV0],
+            dv.reshape(B, H, TKV, D)[:, :, :TKV0])

@@ -52,14 +52,18 @@ def _case(gpu, B, H, TQ, TKV, sparsity, seed):
     return q, k, v, do, out, lse, idx
 
 
-@pytest.mark.parametrize("B,H,TQ,TKV,sparsity", [(1, 2, 512, 1024, 0.25), (2, 1, 1024, 4608, 0.0625),
-                                                 (1, 1, 4096, 36864, 0.0625)])
+@pytest.mark.parametrize("B,H,TQ,TKV,sparsity", [
+    (1, 2, 512, 1024, 0.25), (2, 1, 1024, 4608, 0.0625), (1, 1, 4096, 36864, 0.0625),
+    # ragged lengths of the Triton host: partial last query / key blocks
+    (1, 2, 1024, 4608 + 37, 0.0625), (2, 1, 1000, 1111, 0.25), (1, 1, 4096 - 27, 36856, 0.0625),
+    (1, 1, 40, 65, 1.0),
+])
 def test_backward_matches_oracle(gpu, B, H, TQ, TKV, sparsity):
     print(f"[case] bwd B={B} H={H} TQ={TQ} TKV={TKV} sparsity={sparsity}", flush=True)
     q, k, v, do, out, lse, idx = _case(gpu, B, H, TQ, TKV, sparsity, seed=20)
     # forward state: output and lse against the oracle on the same block lists
     ref_out, _, _, ref_lse = O.sparse_piecewise_attn(q, k, v, sparsity, indices=idx.long().cpu(),
-                                                     return_lse=True)
+                                                     return_lse=True, mode="triton")
     compare_out(out, ref_out)
     dl = (lse.double().cpu() - ref_lse).abs().max().item()
     print(f"[bwd] lse max_abs={dl:.3e}", flush=True)
@@ -68,9 +72,25 @@ def test_backward_matches_oracle(gpu, B, H, TQ, TKV, sparsity):
                                                              out, lse, idx, grad_dtype=torch.float32)
     torch.cuda.synchronize()
     rq, rk, rv = sparse_piecewise_attn_bwd(do, q, k, v, out.cpu(), lse.cpu(), idx.long().cpu())
+    assert dq.shape == q.shape and dk.shape == k.shape and dv.shape == v.shape
     _check_grad("dq", dq, rq)
     _check_grad("dk", dk, rk)
     _check_grad("dv", dv, rv)
+
+
+def test_autograd_function_ragged_lengths(gpu):
+    # the autograd Function at Triton-host lengths: its gradients are those of the
+    # backward entry on the forward's saved state, in the inputs' dtype
+    q, k, v = (_bf16(1, 2, n, 128, seed=60 + i).to(gpu) for i, n in enumerate((1000, 1111, 1111)))
+    do = _bf16(1, 2, 1000, 128, seed=63).to(gpu)
+    qr, kr, vr = (t.clone().requires_grad_(True) for t in (q, k, v))
+    o = SparsePiecewiseAttn1stIntervalsFunction.apply(qr, kr, vr, 0.25, 64)
+    o.backward(do)
+    out, lse, idx = sparse_piecewise_attn_1st_intervals_fwd_hip(q, k, v, 0.25)
+    assert torch.equal(o.detach(), out)
+    want = sparse_piecewise_attn_1st_intervals_bwd_hip(do, q, k, v, out, lse, idx)
+    for got, ref in zip((qr.grad, kr.grad, vr.grad), want):
+        assert got.dtype == torch.bfloat16 and torch.equal(got, ref)
 
 
 def test_backward_quirk_case(gpu):

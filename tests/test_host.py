@@ -97,6 +97,8 @@ def test_size_queries_reject_bad_arguments():
     # ragged lengths (the Triton host) are sized in whole blocks
     assert (_lib.lib().icsa_sparse_piecewise_workspace_size(1, 1, 100, 4645, 128, 0.1)
             == _lib.lib().icsa_sparse_piecewise_workspace_size(1, 1, 128, 4672, 128, 0.1))
+    assert (_lib.lib().icsa_sparse_piecewise_attn_bwd_workspace_size(1, 1, 100, 4645, 128)
+            == _lib.lib().icsa_sparse_piecewise_attn_bwd_workspace_size(1, 1, 128, 4672, 128) > 0)
     assert _lib.lib().icsa_flash_attn_workspace_size(1, 128, 1, 96) < 0
 
 

@@ -6,7 +6,8 @@ Checks other than the oracle's own formulas:
   attention over the selected blocks' rows plus, per unselected block c, one key KC_c / 64
   of multiplicity 64 (logit bias ln 64) with value VC_c / 64.  That attention is built here
   from masks over the full key set and differentiated by torch.autograd; the oracle's
-  forward (out, lse) and backward must match it;
+  forward (out, lse) and backward must match it.  With ragged TQ / TKV (the Triton host) the
+  key set holds only the real rows and KC_c / VC_c sum the real rows of block c;
 * top_k = NKV: dense attention, gradient of float64 scaled_dot_product_attention;
 * lse in log2 units: shifting lse by delta scales every gradient by 2^-delta;
 * brute-force scalar loops (D = 4) of the backward formulas.
@@ -43,15 +44,16 @@ def virtual_attention(q, k, v, idx):
     """Softmax attention over the virtual keys, from masks over [k rows ; KC / 64]."""
     B, H, TQ, D = q.shape
     TKV = k.shape[2]
-    NQ, NKV = TQ // BM, TKV // BM
-    KC = k.view(B, H, NKV, BM, D).sum(3)
-    VC = v.view(B, H, NKV, BM, D).sum(3)
+    NQ, NKV = -(-TQ // BM), -(-TKV // BM)
+    pad = (0, 0, 0, NKV * BM - TKV)
+    KC = F.pad(k, pad).view(B, H, NKV, BM, D).sum(3)
+    VC = F.pad(v, pad).view(B, H, NKV, BM, D).sum(3)
     keys = torch.cat([k, KC / BM], dim=2)
     vals = torch.cat([v, VC / BM], dim=2)
     sel = torch.zeros(B, H, NQ, NKV, dtype=torch.bool)
     sel.scatter_(-1, idx.long(), True)
-    sel_q = sel.repeat_interleave(BM, dim=2)                           # [B,H,TQ,NKV]
-    allow = torch.cat([sel_q.repeat_interleave(BM, dim=3), ~sel_q], dim=3)
+    sel_q = sel.repeat_interleave(BM, dim=2)[:, :, :TQ]                # [B,H,TQ,NKV]
+    allow = torch.cat([sel_q.repeat_interleave(BM, dim=3)[..., :TKV], ~sel_q], dim=3)
     bias = torch.cat([torch.zeros(TKV, dtype=q.dtype), torch.full((NKV,), math.log(BM), dtype=q.dtype)])
     logits = torch.matmul(q, keys.transpose(-2, -1)) / math.sqrt(D) + bias
     logits = logits.masked_fill(~allow, -math.inf)
@@ -76,6 +78,46 @@ def test_backward_is_virtual_attention_gradient(NKV, top_k):
     dq, dk, dv = sparse_piecewise_attn_bwd(do, q, k, v, o.detach(), lse.detach(), idx)
     for got, ref, name in ((dq, qr.grad, "dq"), (dk, kr.grad, "dk"), (dv, vr.grad, "dv")):
         assert torch.allclose(got, ref, atol=1e-11, rtol=1e-9), (name, (got - ref).abs().max().item())
+
+
+@pytest.mark.parametrize("TQ,TKV,top_k", [(3 * BM - 17, 5 * BM - 27, 2), (BM + 1, 7 * BM + 1, 3),
+                                           (40, 2 * BM, 1)])
+def test_ragged_backward_is_virtual_attention_gradient(TQ, TKV, top_k):
+    # Triton-host lengths: the last query block and the last key block are partial
+    B, H, D = 1, 2, 16
+    NQ, NKV = -(-TQ // BM), -(-TKV // BM)
+    q, k, v, do = _inputs(B, H, TQ, TKV, D, seed=TQ + TKV)
+    idx = _random_indices(B, H, NQ, NKV, top_k, seed=9)
+    qr, kr, vr = (t.clone().requires_grad_(True) for t in (q, k, v))
+    o, lse = virtual_attention(qr, kr, vr, idx)
+    (o * do).sum().backward()
+    out_f, _, _, lse_f = O.sparse_piecewise_attn(q, k, v, sparsity=(top_k + 0.5) / (TKV // BM),
+                                                 indices=idx, return_lse=True, mode="triton")
+    assert torch.allclose(out_f, o.detach(), atol=1e-12, rtol=1e-10)
+    assert torch.allclose(lse_f, lse.detach(), atol=1e-12, rtol=1e-10)
+    dq, dk, dv = sparse_piecewise_attn_bwd(do, q, k, v, o.detach(), lse.detach(), idx)
+    assert dq.shape == q.shape and dk.shape == k.shape and dv.shape == v.shape
+    for got, ref, name in ((dq, qr.grad, "dq"), (dk, kr.grad, "dk"), (dv, vr.grad, "dv")):
+        assert torch.allclose(got, ref, atol=1e-11, rtol=1e-9), (name, (got - ref).abs().max().item())
+
+
+def test_ragged_backward_equals_zero_padded_aligned_case():
+    # rows past TKV that are zero keys of a selected block still take part in the aligned
+    # case, so only a selection without the last block makes the two agree; the aligned
+    # gradients of the real rows must then equal the ragged ones
+    B, H, D, TQ, TKV = 1, 1, 8, 2 * BM - 5, 3 * BM - 10
+    q, k, v, do = _inputs(B, H, TQ, TKV, D, seed=4)
+    idx = torch.tensor([[[[0], [1]]]])
+    g = torch.Generator().manual_seed(6)
+    o = torch.randn(B, H, TQ, D, generator=g, dtype=torch.float64)
+    lse = torch.randn(B, H, TQ, generator=g, dtype=torch.float64) + 3.0
+    rag = sparse_piecewise_attn_bwd(do, q, k, v, o, lse, idx)
+    pq = lambda t: F.pad(t, (0, 0, 0, 2 * BM - TQ))
+    pk = lambda t: F.pad(t, (0, 0, 0, 3 * BM - TKV))
+    al = sparse_piecewise_attn_bwd(pq(do), pq(q), pk(k), pk(v), pq(o), F.pad(lse, (0, 2 * BM - TQ)), idx)
+    for a, r, n in zip(al, rag, (TQ, TKV, TKV)):
+        assert torch.allclose(a[:, :, :n], r, atol=1e-12, rtol=1e-10)
+    assert torch.count_nonzero(al[0][:, :, TQ:]) == 0      # zero query rows: no gradient
 
 
 def test_backward_all_selected_is_dense_gradient():
