@@ -208,7 +208,8 @@ icsa_flash_kernel(FlashParams p) {
         for (int i = 0; i < 16; ++i)
           if (32 * sub + acc_row(i, lane) >= mask_from) s[sub][i] = -INFINITY;
     }
-    float rs = 0.f;
+    // four partial sums: a single chain of 32 dependent adds measured 0.4 % slower
+    float rsv[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int sb = 0; sb < 2; ++sb)
 #pragma unroll
@@ -219,9 +220,10 @@ icsa_flash_kernel(FlashParams p) {
           __builtin_amdgcn_sched_barrier(0);
         }
         const float e = __builtin_amdgcn_exp2f(fmaf(s[sb][i], c, -m_ref));
-        rs += e;
+        rsv[i & 3] += e;
         pf[2 * sb + (i >> 3)][i & 7] = (bf16)e;
       }
+    float rs = (rsv[0] + rsv[1]) + (rsv[2] + rsv[3]);
     // The partial sum exceeds FA_PSUM_MAX (or is NaN: the first tile, against m_ref = -inf)
     // only when a score rose far above the reference: then raise the reference of every row
     // whose tile max exceeds it, rescale O and l, and recompute the tile's probabilities.
