@@ -24,6 +24,7 @@ from .hip_host import (  # noqa: F401
     sparse_piecewise_attn_1st_intervals_bwd_hip,
     sparse_piecewise_attn_1st_intervals_fwd_hip,
     sparse_piecewise_attn_1st_intervals_hip,
+    sparse_piecewise_attn_tilelang_hosttopk_hip,
 )
 
 __all__ = [
@@ -31,6 +32,7 @@ __all__ = [
     'editing_sparse_attention',
     'editing_sparse_attention_tilelang',
     'sparse_piecewise_attn_1st_intervals_hip',
+    'sparse_piecewise_attn_tilelang_hosttopk_hip',
     'sparse_piecewise_attn_1st_intervals',
     'SparsePiecewiseAttn1stIntervalsFunction',
     'sparse_piecewise_attn_1st_intervals_fwd_hip',

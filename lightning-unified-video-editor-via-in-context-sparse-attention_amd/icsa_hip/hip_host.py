@@ -134,6 +134,31 @@ def sparse_piecewise_attn_1st_intervals_hip(q: torch.Tensor, k: torch.Tensor, v:
     return (out, idx_out) if return_indices else out
 
 
+@torch.no_grad()
+def sparse_piecewise_attn_tilelang_hosttopk_hip(q, k, v, sparsity=0.0625, BT=64, BV=32, BN=64,
+                                                threads_topk: int = 128, threads_interval: int = 128,
+                                                sorted_topk: bool = False, fused_use_wgmma: bool = False):
+    """The TileLang pipeline entry ``sparse_piecewise_attn_tilelang_hosttopk``
+    (tilelang_host.py:121-226) on MI355X: block sums, ``top_k = max(1, int(sparsity * NKV))``
+    blocks per query block by ``QC KC^T``, exact attention over them plus the first-order
+    interval over the rest.  The reference's two paths (the fused kernel when ``BV == Vdim``,
+    the top-k + interval kernel pair otherwise) compute the same function; here one kernel
+    serves both, so ``BV`` only has to divide Vdim.  ``BN`` is the interval chunk size,
+    which decides where the non-rescaled interval terms take their running max: 64 is the
+    one this kernel implements (the reference's default and the value every reference
+    caller passes).  ``threads_*``, ``sorted_topk`` (the exact loop's visiting order only
+    changes rounding) and ``fused_use_wgmma`` select reference launch variants and have
+    no effect here."""
+    assert q.dtype == k.dtype == v.dtype == torch.bfloat16
+    _require(q.ndim == 4 and k.ndim == 4 and v.ndim == 4, "q, k, v must be 4-D [B, H, T, D]")
+    TQ, TKV, Vdim = q.shape[2], k.shape[2], v.shape[3]
+    assert TQ % BT == 0 and TKV % BT == 0, "TQ/TKV must be divisible by BT"
+    assert Vdim % BV == 0, "Vdim must be divisible by BV"
+    _require(BT == BLOCK_M, f"BT={BT} unsupported (the kernels use 64-row blocks)")
+    _require(BN == 64, f"BN={BN} unsupported (the interval runs over chunks of 64 blocks)")
+    return sparse_piecewise_attn_1st_intervals_hip(q, k, v, sparsity, BT)
+
+
 def _check_sparse_args(q, k, v, block_size, aligned=True):
     """The TileLang host's argument checks (tilelang_host.py:251-259); ``aligned=False``
     drops the multiple-of-64 lengths the Triton host does not need."""

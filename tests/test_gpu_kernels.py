@@ -6,7 +6,8 @@ import torch
 
 import oracle as O
 from icsa_hip import (flash_attn_func, gather_kv, pool,
-                      sparse_piecewise_attn_1st_intervals_hip)
+                      sparse_piecewise_attn_1st_intervals_hip,
+                      sparse_piecewise_attn_tilelang_hosttopk_hip)
 from icsa_hip.hip_host import IcsaArgumentError
 from parity import GAP, compare_out, l3_scale
 
@@ -79,6 +80,19 @@ def test_sparse_piecewise_host(gpu, TQ, TKV, sparsity):
     top_k = idx.shape[-1]
     assert O.check_topk_valid(scores / l3_scale(128), idx.long().cpu(), top_k, GAP, ordered=False).all()
     compare_out(out, ref)
+
+
+def test_tilelang_hosttopk_entry(gpu):
+    # sparse_piecewise_attn_tilelang_hosttopk's two reference paths (BV == Vdim: fused kernel;
+    # BV < Vdim: top-k + interval kernels) compute one function; both map onto the same kernel
+    q, k, v = (_bf16(1, 2, n, 128, seed=30 + i).to(gpu) for i, n in enumerate((512, 4608, 4608)))
+    want = sparse_piecewise_attn_1st_intervals_hip(q, k, v, 0.0625, 64)
+    for bv, srt in ((32, False), (128, True)):
+        got = sparse_piecewise_attn_tilelang_hosttopk_hip(q, k, v, 0.0625, BT=64, BV=bv, BN=64,
+                                                          sorted_topk=srt)
+        assert torch.equal(got, want)
+    with pytest.raises(IcsaArgumentError):
+        sparse_piecewise_attn_tilelang_hosttopk_hip(q, k, v, BN=32)
 
 
 def test_sparse_piecewise_quirk_case(gpu):

@@ -167,6 +167,21 @@ def test_host_functions_mirror_reference_asserts():
         flash_attn_func(x, x, x, causal=True)
 
 
+def test_tilelang_hosttopk_mirrors_reference_asserts():
+    from icsa_hip import sparse_piecewise_attn_tilelang_hosttopk_hip as hosttopk
+    x = torch.zeros(1, 1, 128, 128, dtype=torch.bfloat16)
+    with pytest.raises(AssertionError):          # reference: bf16 inputs
+        hosttopk(x.float(), x, x)
+    with pytest.raises(AssertionError):          # reference: TQ/TKV divisible by BT
+        hosttopk(x[:, :, :100], x, x)
+    with pytest.raises(AssertionError):          # reference: Vdim divisible by BV
+        hosttopk(x, x, x, BV=48)
+    with pytest.raises(IcsaArgumentError, match="BN"):
+        hosttopk(x, x, x, BN=32)
+    with pytest.raises(IcsaArgumentError, match="GPU"):
+        hosttopk(x, x, x)
+
+
 def test_product_package_never_imports_the_oracle():
     pat = re.compile(r"^\s*(from|import)\s+oracle\b", re.M)
     for dirpath, _, files in os.walk(PKG):
