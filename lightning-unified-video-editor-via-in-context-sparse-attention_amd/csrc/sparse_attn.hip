@@ -304,11 +304,12 @@ icsa_sparse_kernel(SparseParams p) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) o[ds][i] *= a;
   };
-  // interval scores of one chunk: z = s c / 64, -inf for selected blocks and blocks >= NKV
+  // interval chunk: raw scores of selected blocks and blocks >= NKV set to -inf; returns the
+  // chunk max in log2 units (q . KC c / 64)
+  const float c64 = p.scale_log2 * (1.0f / 64.0f);
   auto interval_z = [&](int c) -> float {
     const unsigned long long selm = sel_l[c];
     const int j0 = c * ATT_BN;
-    const float c64 = p.scale_log2 * (1.0f / 64.0f);
     float mx = -INFINITY;
 #pragma unroll
     for (int sub = 0; sub < 2; ++sub)
@@ -316,11 +317,13 @@ icsa_sparse_kernel(SparseParams p) {
       for (int i = 0; i < 16; ++i) {
         const int jj = 32 * sub + acc_row(i, lane);
         const bool masked = (j0 + jj >= p.NKV) || ((selm >> jj) & 1ull);
-        const float z = masked ? -INFINITY : s[sub][i] * c64;
+        const float z = masked ? -INFINITY : s[sub][i];
         s[sub][i] = z;
         mx = fmaxf(mx, z);
       }
-    return xhalf_max(mx);
+    // the scale is positive, so the max of the scaled scores is the scaled max (the same
+    // rounded value): the exponentials take s * c64 - m in one fma
+    return xhalf_max(mx) * c64;
   };
 
   const float c = p.scale_log2;
@@ -420,7 +423,7 @@ icsa_sparse_kernel(SparseParams p) {
     for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const float e = __builtin_amdgcn_exp2f(s[sub][i] - m_c);
+        const float e = __builtin_amdgcn_exp2f(fmaf(s[sub][i], c64, -m_c));
         rs += e;
         pf[2 * sub + (i >> 3)][i & 7] = (bf16)e;
       }
