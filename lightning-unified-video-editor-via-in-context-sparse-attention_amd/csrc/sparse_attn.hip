@@ -308,16 +308,22 @@ icsa_sparse_kernel(SparseParams p) {
   // chunk max in log2 units (q . KC c / 64)
   const float c64 = p.scale_log2 * (1.0f / 64.0f);
   auto interval_z = [&](int c) -> float {
-    const unsigned long long selm = sel_l[c];
-    const int j0 = c * ATT_BN;
+    // masked blocks of the chunk as one uniform 64-bit word (selected, or >= NKV)
+    unsigned long long mb = sel_l[c];
+    const int n_real = p.NKV - c * ATT_BN;
+    if (n_real < ATT_BN) mb |= ~0ull << n_real;
+    // accumulator element i of sub-tile sub is block 32 sub + 8 (i / 4) + 4 hl + i % 4: bit
+    // 8 (i / 4) + i % 4 of word sub of mb >> 4 hl, spread to a full mask that selects -inf
+    const unsigned long long ml = mb >> (4 * hl);
+    const unsigned wd[2] = {(unsigned)ml, (unsigned)(ml >> 32)};
     float mx = -INFINITY;
 #pragma unroll
     for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const int jj = 32 * sub + acc_row(i, lane);
-        const bool masked = (j0 + jj >= p.NKV) || ((selm >> jj) & 1ull);
-        const float z = masked ? -INFINITY : s[sub][i];
+        const int k = 8 * (i >> 2) + (i & 3);
+        const unsigned all = (unsigned)((int)(wd[sub] << (31 - k)) >> 31);
+        const float z = __uint_as_float((all & 0xff800000u) | (__float_as_uint(s[sub][i]) & ~all));
         s[sub][i] = z;
         mx = fmaxf(mx, z);
       }
