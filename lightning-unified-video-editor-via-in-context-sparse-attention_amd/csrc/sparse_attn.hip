@@ -57,7 +57,7 @@
 #define SP_STAGE_BYTES (32 * O_LDS_STRIDE * 4)
 #define SP_BUF_BYTES (SP_STAGE_BYTES > K_TILE_BYTES ? SP_STAGE_BYTES : K_TILE_BYTES)
 #define SP_RESCALE_LOG2 8.0f
-#define SP_PF 2                          // MFMA operand read-ahead (steps); 3 spills at 256 VGPRs
+#define SP_PF 2                          // MFMA operand read-ahead (steps); 3 or 4 measured no faster
 #define SP_DMA_PER_TILE 8                // LDS-DMA instructions per wave per K or V tile
 #ifndef SP_SWEEP_CONC
 #define SP_SWEEP_CONC 256                // sweep start advances NKV / SP_SWEEP_CONC per launch
