@@ -265,13 +265,18 @@ __global__ void __launch_bounds__(BW_THREADS) icsa_sparse_bwd_dq_kernel(SparseBw
         }
     } else {                                           // unselected block sums: score / 64, dS / 64
       const int ch = t - n_ex;
-      const unsigned long long selm = sel_l[ch];
+      // masked blocks of the chunk (selected, or >= NKV) as one word; element e of sub-tile
+      // sub is bit 8 (e / 4) + e % 4 of word sub of that word >> 4 hl
+      unsigned long long mb = sel_l[ch];
+      const int n_real = p.NKV - ch * ICSA_BLOCK;
+      if (n_real < ICSA_BLOCK) mb |= ~0ull << n_real;
+      const unsigned long long ml = mb >> (4 * (lane >> 5));
+      const unsigned wd[2] = {(unsigned)ml, (unsigned)(ml >> 32)};
 #pragma unroll
       for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
-          const int jj = 32 * sub + acc_row(e, lane);
-          const bool masked = (ch * ICSA_BLOCK + jj >= p.NKV) || ((selm >> jj) & 1ull);
+          const bool masked = (wd[sub] >> (8 * (e >> 2) + (e & 3))) & 1u;
           const float pr = masked ? 0.f : __builtin_amdgcn_exp2f(fmaf(s[sub][e], c64, -lse));
           dsf[2 * sub + (e >> 3)][e & 7] = (bf16)(pr * (dp[sub][e] - 64.0f * dd) * (1.0f / 64.0f));
         }
