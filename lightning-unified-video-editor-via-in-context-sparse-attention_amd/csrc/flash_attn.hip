@@ -19,7 +19,7 @@
 // SIMD feeds the matrix pipe while the other keeps the vector ALU busy ("ping-pong").
 //
 // Tiles arrive by direct global->LDS buffer loads (LDS DMA: lane l of a load lands at
-// M0 + 16 l), triple buffered.  Issuing LDS DMA blocks the issuing wave while the CU's
+// M0 + 16 l), four buffers deep.  Issuing LDS DMA blocks the issuing wave while the CU's
 // vector-memory path takes earlier requests, so only waves in their SOFT phase issue it,
 // one 1-KB segment between every 8 exponentials (group 1: K tiles, group 0: V^T tiles; the
 // slot schedule below).  The LDS XOR swizzle is applied on the global side: each lane
@@ -39,7 +39,7 @@
 #define FA_THREADS (FA_WAVES * 64)
 #define FA_QBLK_PER_WG (FA_WAVES / 2)
 #define FA_STAGE_BYTES (FA_WAVES * 32 * O_LDS_STRIDE * 4)    // epilogue staging, all waves
-#define FA_NBUF 3                                            // K and V^T tile buffers
+#define FA_NBUF 4                                            // K and V^T tile buffers
 #define FA_TILE_BYTES (FA_NBUF * (K_TILE_BYTES + V_TILE_BYTES))
 #define FA_MAX_SEL 4096                                      // extra tiles (LDS list)
 #define FA_JUNK_OFF (FA_TILE_BYTES + 4 * FA_MAX_SEL)         // landing area of disabled DMA
@@ -172,7 +172,6 @@ icsa_flash_kernel(FlashParams p) {
   __amdgpu_buffer_rsrc_t dma_rs = make_rsrc(kb, 0);
   unsigned char* dma_dst = smem;
   bool dma_on = false;
-  int dma_kvalid = ATT_BN;
   // sets up this wave's part of tile j: K(j) for group 1, V^T(j) for group 0
   auto dma_setup = [&](int j) {
     dma_on = j < n_tiles;
@@ -187,7 +186,6 @@ icsa_flash_kernel(FlashParams p) {
       const int64_t k_bytes = k_valid > 0 ? ((int64_t)(k_valid - 1) * p.k_ss + ICSA_D) * 2 : 0;
       dma_rs = make_rsrc(kb + (int64_t)tok0 * p.k_ss, k_bytes);
       dma_dst = kbuf(j) + dw * 4096;
-      dma_kvalid = k_valid;
     } else {
       dma_rs = make_rsrc(vb + (int64_t)j * ATT_BN, ((int64_t)(ICSA_D - 1) * p.vt_sd + ATT_BN) * 2);
       dma_dst = vbuf(j) + dw * 4096;
@@ -261,20 +259,16 @@ icsa_flash_kernel(FlashParams p) {
   // issuing wave while the CU's vector-memory path drains earlier requests (about 22
   // s_memtime ticks per 1-KB instruction), so the tile DMA is issued only by waves in their
   // SOFT phase, one segment between every 8 exponentials, never by a GEMM wave:
-  //   K(j): group 1 during SOFT(j - 3), slot 2j - 4; waited for by group 1 at the end of its
+  //   K(j): group 1 during SOFT(j - 4), slot 2j - 6; waited for by group 1 at the end of its
   //         GEMM(j - 1), slot 2j - 1; read in slots 2j (group 0) and 2j + 1 (group 1);
-  //   V(j): group 0 during SOFT(j - 1), slot 2j - 1; waited for by group 0 at the end of its
+  //   V(j): group 0 during SOFT(j - 2), slot 2j - 3; waited for by group 0 at the end of its
   //         SOFT(j), slot 2j + 1; read (as PV(j)) in slots 2j + 2 and 2j + 3.
-  // Three buffers per kind: K(j) overwrites K(j - 3), last read in slot 2j - 5; V(j)
-  // overwrites V(j - 3), last read (PV(j - 3)) in slot 2j - 3.  Loads complete
-  // in issue order, so vmcnt(4) waits for all but this wave's newest tile.  Slots past the
-  // last tile issue empty-range loads into a junk LDS area (the issue stays branch-free).
+  // Four buffers per kind: K(j) overwrites K(j - 4), last read in slot 2j - 7; V(j)
+  // overwrites V(j - 4), last read (PV(j - 4)) in slot 2j - 5.  Loads complete in issue
+  // order, so vmcnt(8) waits for all but this wave's two newest tiles.  Slots past the last
+  // tile issue empty-range loads into a junk LDS area (the issue stays branch-free).
   const bool compute = q_valid > 0;
   const bool lag = group == 1;
-  auto wait_tile = [&](bool newer) {
-    if (newer) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
-    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  };
   // zero key rows >= k_valid of a group-1 wave's K segments (rows 16 dw .. 16 dw + 15)
   auto fill_tail4 = [&](int j, int k_valid) {
     if (k_valid >= ATT_BN) return;
@@ -289,44 +283,38 @@ icsa_flash_kernel(FlashParams p) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) dma_seg(i);
   };
-  // prologue: group 1 issues K(0), K(1); group 0 issues V(0); K(0) is made visible
-  int kv_a = ATT_BN, kv_b = ATT_BN;       // group 1: valid rows of K(k + 1) and K(k + 2)
+  // wait for a tile, leaving the `newer` (at most two) tiles issued after it in flight
+  auto wait_n = [&](int newer) {
+    if (newer >= 2) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    else if (newer == 1) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  };
+  auto kvalid_of = [&](int j) -> int { return min(ATT_BN, p.Sk - tile_tok0(j)); };
   if (lag) {
-    dma_setup(0);
-    const int kv0 = dma_kvalid;
-    issue_all();
-    dma_setup(1);
-    kv_a = dma_kvalid;
-    issue_all();
-    wait_tile(1 < n_tiles);
-    fill_tail4(0, kv0);
+    for (int j = 0; j < 3; ++j) { dma_setup(j); issue_all(); }
+    wait_n(min(2, n_tiles - 1));          // K(0): K(1), K(2) are newer when they exist
+    fill_tail4(0, kvalid_of(0));
   } else {
-    dma_setup(0);
-    issue_all();
+    dma_setup(0); issue_all();
+    dma_setup(1); issue_all();
   }
   ATT_BARRIER();
-  if (lag) {                               // slot 0 for group 1: K(2) ("SOFT(-1)")
-    dma_setup(2);
-    kv_b = dma_kvalid;
+  if (lag) {                               // slot 0 for group 1: K(3)
+    dma_setup(3);
     issue_all();
     ATT_BARRIER();
   }
   for (int k = 0; k <= n_tiles; ++k) {
     if (compute) gemm(k);
-    // group 1, end of slot 2k + 1: K(k + 1) (K(k + 2) is newer when it exists)
-    if (lag && k + 1 < n_tiles) {
-      wait_tile(k + 2 < n_tiles);
-      fill_tail4(k + 1, kv_a);
+    if (lag && k + 1 < n_tiles) {          // K(k + 1); K(k + 2), K(k + 3) are newer
+      wait_n(min(2, n_tiles - (k + 2)));
+      fill_tail4(k + 1, kvalid_of(k + 1));
     }
     ATT_BARRIER();
-    // SOFT(k): group 0 issues V(k + 1), group 1 issues K(k + 3)
-    dma_setup(lag ? k + 3 : k + 1);
-    const int kv_new = dma_kvalid;
+    dma_setup(lag ? k + 4 : k + 2);
     if (compute && k < n_tiles) soft(k);
     else issue_all();
-    // group 0, end of slot 2k + 1: V(k) (V(k + 1) is newer when it exists)
-    if (!lag && k < n_tiles) wait_tile(k + 1 < n_tiles);
-    if (lag) { kv_a = kv_b; kv_b = kv_new; }
+    if (!lag && k < n_tiles) wait_n(min(2, n_tiles - (k + 1)));   // V(k); V(k + 1), V(k + 2) newer
     ATT_BARRIER();
   }
   if (!lag) ATT_BARRIER();       // group 0's extra slot
