@@ -166,8 +166,15 @@ struct SparseParams {
   OutView out;
   float scale_log2;
   float* lse;                        // optional [BH, Sq]: m + log2(l + g_l) per query (log2 units)
+  // optional [BH, kc_bound_n] partial maxima of |KC_j| (launch_kc_bound): a workgroup whose
+  // rows all satisfy |q| max |KC_j| c / 64 < exact max skips the interval max pass
+  const float* kc_bound; int kc_bound_n;
 };
 hipError_t launch_sparse(const SparseParams& p, hipStream_t stream);
+// out[bh * G + y] = max over new-KV blocks j = y, y + G, ... < NKV of the L2 norm of the
+// bf16 row kc[bh, j, :] (fp32 arithmetic); G = min(8, NKV) is returned in *G
+hipError_t launch_kc_bound(const bf16* kc, int BH, int NKV, int NKVp, float* out, int* G,
+                           hipStream_t stream);
 
 // ---------------------------------------------------------------- backward (sparse_bwd.hip)
 // Gradients of the sparse piecewise attention (triton_kernels.py:265-486, 541-598) without

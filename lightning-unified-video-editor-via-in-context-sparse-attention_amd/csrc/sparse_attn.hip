@@ -18,7 +18,10 @@
 // and pass 2 recomputes the same running max chunk by chunk and accumulates the
 // non-rescaled g terms straight into the output accumulator.  That costs one extra
 // Q.KC product per chunk and frees the separate g accumulator (64 registers), which is
-// what lets two waves share each SIMD.
+// what lets two waves share each SIMD.  Pass 1 is skipped when a Cauchy-Schwarz bound,
+// |q| max_j |KC_j| c / 64 (max_j |KC_j| per head from icsa_kc_bound_kernel), lies below the
+// exact max of every row of the workgroup: then the running max cannot rise and
+// m_final = m_exact, bit for bit.
 //
 // The new KV is read in place: new-KV block j lives at source block kvmap[j] of the
 // K / V buffers -- target blocks and the selected source blocks of the original
@@ -78,6 +81,7 @@ icsa_sparse_kernel(SparseParams p) {
   __shared__ int nkv_l[SP_MAX_TOPK];                  // its new-KV block (V^T column block; -1: zeros)
   __shared__ unsigned long long sel_l[SP_MAX_CHUNKS];  // selected new-KV blocks per chunk
   __shared__ int rot_l;                               // exact tiles visited from list entry rot_l
+  __shared__ int skip_l[2];                           // per wave: the interval max pass is not needed
 
   const int n_work = p.B * p.H * p.n_qblk;
   const int work = xcd_remap(blockIdx.x, n_work);
@@ -389,12 +393,37 @@ icsa_sparse_kernel(SparseParams p) {
     pv();
     kv_pending = kv_next;
   }
-  ATT_BARRIER();                           // V buffer free
+  // Pass 1 only finds the final running max.  Every interval score satisfies
+  // |q . KC_j| <= |q| |KC_j| (Cauchy-Schwarz; the fp32 sums stay within 2^-10 of it), so
+  // when |q| max_j |KC_j| c / 64 < m_true for every row of the workgroup, the running max
+  // never leaves m_true and pass 1 is skipped (bit-identical result).  Rows past the query
+  // end take no part.
+  if (p.kc_bound != nullptr) {
+    float kb = 0.f;
+    for (int g = 0; g < p.kc_bound_n; ++g) kb = fmaxf(kb, p.kc_bound[(int64_t)bh * p.kc_bound_n + g]);
+    float qn2 = 0.f;
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float x = bf2f(qf[kk][e]);
+        qn2 = fmaf(x, x, qn2);
+      }
+    const float bound = sqrtf(xhalf_sum(qn2)) * kb * c64 * (1.0f + 0x1p-10f);
+    const bool safe = bound < m_true || li >= q_valid;
+    if (lane == 0) skip_l[wave] = __ballot(!safe) == 0ull ? 1 : 0;
+  } else if (lane == 0) {
+    skip_l[wave] = 0;
+  }
+  ATT_BARRIER();                           // V buffer free; skip_l ready
   issue_v(T2);                             // pass 2's first V tile, after K(T1)
+  const bool skip1 = (skip_l[0] & skip_l[1]) != 0;
 
   // ---- 2a. interval pass 1: running max over the chunks ----
+  // (K(T1) is chunk 0 of KC, the same tile as pass 2's first K(T2): a skipped pass 1
+  // leaves it in flight for pass 2)
   float m_run = m_true;
-  for (int ch = 0; ch < nc; ++ch) {
+  for (int ch = 0; ch < (skip1 ? 0 : nc); ++ch) {
     if (ch == 0) SP_WAIT_OLDER();          // V(T2) was issued after K(T1)
     else SP_WAIT_ALL();
     ATT_BARRIER();
@@ -455,6 +484,39 @@ icsa_sparse_kernel(SparseParams p) {
     const float* oc = p.out_c ? p.out_c + ((int64_t)bh * p.nb_q + qblk) * ICSA_D : nullptr;
     store_rows(o_lds, p.out, b, h, qtok0, q_valid, oc, p.alpha);
   }
+}
+
+// One workgroup per (b, h) and residue y of the block index modulo G: each thread takes
+// whole rows (16 loads of 16 bytes), the workgroup maximum of the squared norms goes
+// through an LDS atomic (non-negative floats order like their bit patterns).
+__global__ void __launch_bounds__(256) icsa_kc_bound_kernel(const bf16* kc, int NKV, int NKVp, float* out) {
+  __shared__ unsigned mx;
+  const int bh = blockIdx.x, y = blockIdx.y, G = gridDim.y;
+  if (threadIdx.x == 0) mx = 0u;
+  __syncthreads();
+  float best = 0.f;
+  for (int j = y + G * (int)threadIdx.x; j < NKV; j += G * (int)blockDim.x) {
+    const bf16* row = kc + ((int64_t)bh * NKVp + j) * ICSA_D;
+    float n2 = 0.f;
+#pragma unroll
+    for (int c = 0; c < ICSA_D / 8; ++c) {
+      const bf16x8 v = *reinterpret_cast<const bf16x8*>(row + 8 * c);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) n2 = fmaf(bf2f(v[e]), bf2f(v[e]), n2);
+    }
+    best = fmaxf(best, n2);
+  }
+  atomicMax(&mx, __float_as_uint(best));
+  __syncthreads();
+  if (threadIdx.x == 0) out[(int64_t)bh * G + y] = sqrtf(__uint_as_float(mx));
+}
+
+hipError_t launch_kc_bound(const bf16* kc, int BH, int NKV, int NKVp, float* out, int* G,
+                           hipStream_t stream) {
+  *G = NKV < 8 ? NKV : 8;
+  if (BH <= 0 || NKV <= 0) return hipSuccess;
+  hipLaunchKernelGGL(icsa_kc_bound_kernel, dim3(BH, *G), dim3(256), 0, stream, kc, NKV, NKVp, out);
+  return hipGetLastError();
 }
 
 hipError_t launch_sparse(const SparseParams& p, hipStream_t stream) {

@@ -95,6 +95,44 @@ def test_tilelang_hosttopk_entry(gpu):
         sparse_piecewise_attn_tilelang_hosttopk_hip(q, k, v, BN=32)
 
 
+def _interval_skip_margin(q, k, idx):
+    """Per query block (q, k: [B, H, T, D] bf16, idx: [B, H, NQ, top_k] exact blocks): the
+    minimum over its rows of m_exact - |q| max_j |KC_j| c / 64, in log2 units, with KC_j the
+    bf16 block sums of the keys.  Positive: the Cauchy-Schwarz bound proves that no interval
+    score reaches the exact max, and the kernel skips its interval max pass for the block;
+    negative: it runs both interval passes."""
+    c = math.log2(math.e) / math.sqrt(q.shape[-1])
+    B, H, TQ, D = q.shape
+    NKV = k.shape[2] // 64
+    kc = k.float().view(B, H, NKV, 64, D).sum(3).to(torch.bfloat16).float()
+    bound = q.float().norm(dim=-1) * kc.norm(dim=-1).amax(-1)[..., None] * c / 64
+    out = []
+    for b in range(B):
+        for h in range(H):
+            keys = k[b, h].float().view(NKV, 64, D)
+            for blk in range(TQ // 64):
+                rows = q[b, h, 64 * blk:64 * blk + 64].float()
+                m = (rows @ keys[idx[b, h, blk].long()].reshape(-1, D).T).amax(-1) * c
+                out.append((m - bound[b, h, 64 * blk:64 * blk + 64]).min().item())
+    return out
+
+
+def test_sparse_piecewise_interval_bound_skip(gpu):
+    # Random queries and keys: the bound holds for every query block, so every workgroup
+    # skips the interval max pass; the result must still be the oracle's.
+    print("[case] sparse interval-bound skip path", flush=True)
+    TQ, TKV = 256, 64 * 64
+    q, k, v = _bf16(1, 2, TQ, 128, seed=31), _bf16(1, 2, TKV, 128, seed=32), _bf16(1, 2, TKV, 128, seed=33)
+    g = torch.Generator().manual_seed(34)
+    idx = torch.stack([torch.randperm(64, generator=g)[:4].sort().values for _ in range(2 * TQ // 64)])
+    idx = idx.view(1, 2, TQ // 64, 4).to(torch.int32)
+    assert min(_interval_skip_margin(q, k, idx)) > 0.25
+    out = sparse_piecewise_attn_1st_intervals_hip(q.to(gpu), k.to(gpu), v.to(gpu), 0.0625,
+                                                  indices=idx.to(gpu))
+    ref, _, _ = O.sparse_piecewise_attn(q, k, v, 0.0625, indices=idx.long())
+    compare_out(out, ref)
+
+
 def test_sparse_piecewise_quirk_case(gpu):
     # Keys of a late chunk align with the queries: the interval's running max rises after
     # earlier chunks were accumulated, which the reference does not rescale.  The oracle
@@ -107,6 +145,7 @@ def test_sparse_piecewise_quirk_case(gpu):
     k[0, 0, 64 * 150:64 * 151] = (20.0 * q[0, 0].float().mean(0)).expand(64, 128).to(torch.bfloat16)
     v = _bf16(1, 1, TKV, 128, seed=15)
     idx = torch.arange(12, dtype=torch.int32).view(1, 1, 1, 12)
+    assert max(_interval_skip_margin(q, k, idx)) < -1.0   # both interval passes run
     out = sparse_piecewise_attn_1st_intervals_hip(q.to(gpu), k.to(gpu), v.to(gpu), 0.0625,
                                                   indices=idx.to(gpu))
     ref, _, _ = O.sparse_piecewise_attn(q, k, v, 0.0625, indices=idx.long())
