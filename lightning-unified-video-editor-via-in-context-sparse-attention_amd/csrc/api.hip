@@ -396,7 +396,7 @@ int editing_impl(ICSA_EDITING_ARGS, void* const* stage_events, const float* qsum
     s.out_c = cp.out_c; s.nb_q = z.NB;
     s.alpha = av; s.out = ov; s.scale_log2 = scale_log2; s.lse = nullptr;
     s.mask_tail = 0;                   // zero-padded new KV attended with logit 0 (TileLang)
-    // the level-3 score rows are free again: BH * min(8, NKV) floats of them hold the |KC_j|
+    // the level-3 score rows are free again: BH * min(8, cdiv(NKV, 16)) floats of them hold the |KC_j|
     // bound of the interval pass
     s.kc_bound = reinterpret_cast<float*>(WS(ICSA_WS_L3S));
     ICSA_HIP_TRY(launch_kc_bound(np.kc, BH, z.NKV, z.NKVp, reinterpret_cast<float*>(WS(ICSA_WS_L3S)),
@@ -743,7 +743,7 @@ static int sparse_piecewise_impl(
   s.scale_log2 = kLog2e / std::sqrt((float)ICSA_D);
   s.lse = lse_out;
   s.mask_tail = triton;
-  // the block top-k score rows are free again: BH * min(8, NKV) floats of them hold the
+  // the block top-k score rows are free again: BH * min(8, cdiv(NKV, 16)) floats of them hold the
   // |KC_j| bound of the interval pass
   s.kc_bound = reinterpret_cast<float*>(ws + L.scores);
   ICSA_HIP_TRY(launch_kc_bound(np.kc, BH, NKV, NKVp, reinterpret_cast<float*>(ws + L.scores),

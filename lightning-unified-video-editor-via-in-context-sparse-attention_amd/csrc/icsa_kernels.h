@@ -171,8 +171,9 @@ struct SparseParams {
   const float* kc_bound; int kc_bound_n;
 };
 hipError_t launch_sparse(const SparseParams& p, hipStream_t stream);
-// out[bh * G + y] = max over new-KV blocks j = y, y + G, ... < NKV of the L2 norm of the
-// bf16 row kc[bh, j, :] (fp32 arithmetic); G = min(8, NKV) is returned in *G
+// out[bh * G + y] = max over the new-KV blocks j < NKV with (j / 16) % G == y of the L2
+// norm of the bf16 row kc[bh, j, :] (fp32 arithmetic); G = min(8, cdiv(NKV, 16)) is
+// returned in *G (at most NKV, so BH * G floats fit wherever BH * NKV do)
 hipError_t launch_kc_bound(const bf16* kc, int BH, int NKV, int NKVp, float* out, int* G,
                            hipStream_t stream);
 

@@ -127,6 +127,13 @@ icsa_sparse_kernel(SparseParams p) {
   bf16x8 qf[8];
   load_q_frags(qf, p.q + (int64_t)b * p.q_sb + (int64_t)qtok0 * p.q_ss + (int64_t)h * p.q_sh, p.q_ss,
                q_valid);
+  // max_j |KC_j| of the head (used after the exact loop; loaded now so the exact loop hides
+  // the load)
+  float kc_max = INFINITY;
+  if (p.kc_bound != nullptr) {
+    kc_max = 0.f;
+    for (int g = 0; g < p.kc_bound_n; ++g) kc_max = fmaxf(kc_max, p.kc_bound[(int64_t)bh * p.kc_bound_n + g]);
+  }
 
   // ---- DMA segments ----
   // K tiles and V row tiles: this wave's rows 32 w .. 32 w + 31 in 8 one-KB segments of 4
@@ -399,8 +406,6 @@ icsa_sparse_kernel(SparseParams p) {
   // never leaves m_true and pass 1 is skipped (bit-identical result).  Rows past the query
   // end take no part.
   if (p.kc_bound != nullptr) {
-    float kb = 0.f;
-    for (int g = 0; g < p.kc_bound_n; ++g) kb = fmaxf(kb, p.kc_bound[(int64_t)bh * p.kc_bound_n + g]);
     float qn2 = 0.f;
 #pragma unroll
     for (int kk = 0; kk < 8; ++kk)
@@ -409,7 +414,7 @@ icsa_sparse_kernel(SparseParams p) {
         const float x = bf2f(qf[kk][e]);
         qn2 = fmaf(x, x, qn2);
       }
-    const float bound = sqrtf(xhalf_sum(qn2)) * kb * c64 * (1.0f + 0x1p-10f);
+    const float bound = sqrtf(xhalf_sum(qn2)) * kc_max * c64 * (1.0f + 0x1p-10f);
     const bool safe = bound < m_true || li >= q_valid;
     if (lane == 0) skip_l[wave] = __ballot(!safe) == 0ull ? 1 : 0;
   } else if (lane == 0) {
@@ -486,24 +491,27 @@ icsa_sparse_kernel(SparseParams p) {
   }
 }
 
-// One workgroup per (b, h) and residue y of the block index modulo G: each thread takes
-// whole rows (16 loads of 16 bytes), the workgroup maximum of the squared norms goes
-// through an LDS atomic (non-negative floats order like their bit patterns).
+// Workgroup (b, h, y) takes the rows j = 16 (y + G i) + r, r = 0 .. 15 (i = 0, 1, ...): 16
+// lanes per row, one 16-byte chunk each, the squared norm summed over the 16 lanes with
+// lane shuffles; the workgroup maximum goes through an LDS atomic (non-negative floats
+// order like their bit patterns).
 __global__ void __launch_bounds__(256) icsa_kc_bound_kernel(const bf16* kc, int NKV, int NKVp, float* out) {
   __shared__ unsigned mx;
   const int bh = blockIdx.x, y = blockIdx.y, G = gridDim.y;
+  const int r = threadIdx.x >> 4, ch = threadIdx.x & 15;
   if (threadIdx.x == 0) mx = 0u;
   __syncthreads();
   float best = 0.f;
-  for (int j = y + G * (int)threadIdx.x; j < NKV; j += G * (int)blockDim.x) {
-    const bf16* row = kc + ((int64_t)bh * NKVp + j) * ICSA_D;
+  for (int j0 = 16 * y; j0 < NKV; j0 += 16 * G) {
+    const int j = j0 + r;
     float n2 = 0.f;
-#pragma unroll
-    for (int c = 0; c < ICSA_D / 8; ++c) {
-      const bf16x8 v = *reinterpret_cast<const bf16x8*>(row + 8 * c);
+    if (j < NKV) {
+      const bf16x8 v = *reinterpret_cast<const bf16x8*>(kc + ((int64_t)bh * NKVp + j) * ICSA_D + 8 * ch);
 #pragma unroll
       for (int e = 0; e < 8; ++e) n2 = fmaf(bf2f(v[e]), bf2f(v[e]), n2);
     }
+#pragma unroll
+    for (int w = 1; w < 16; w <<= 1) n2 += __shfl_xor(n2, w);
     best = fmaxf(best, n2);
   }
   atomicMax(&mx, __float_as_uint(best));
@@ -513,7 +521,8 @@ __global__ void __launch_bounds__(256) icsa_kc_bound_kernel(const bf16* kc, int 
 
 hipError_t launch_kc_bound(const bf16* kc, int BH, int NKV, int NKVp, float* out, int* G,
                            hipStream_t stream) {
-  *G = NKV < 8 ? NKV : 8;
+  const int groups = (NKV + 15) / 16;                 // 16-row groups
+  *G = groups < 8 ? groups : 8;
   if (BH <= 0 || NKV <= 0) return hipSuccess;
   hipLaunchKernelGGL(icsa_kc_bound_kernel, dim3(BH, *G), dim3(256), 0, stream, kc, NKV, NKVp, out);
   return hipGetLastError();
