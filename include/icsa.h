@@ -93,7 +93,8 @@ enum icsa_ws_slot {
   ICSA_WS_NKSUM,      /* f32 [B*H, NKV, D]  (t % 64 != 0 only)                       */
   ICSA_WS_NVSUM,      /* f32 [B*H, NKV, D]  (t % 64 != 0 only)                       */
   ICSA_WS_COLP,       /* f32 [B*H, ceil(n_t/64), n_s] source-column mass per target strip */
-  ICSA_WS_L3S,        /* f32 [B*H, n_diffuse, NKV] level-3 block scores (scratch)    */
+  ICSA_WS_L3S,        /* f32 [B*H, n_diffuse, NKV] level-3 block scores (scratch;    */
+                      /* afterwards its first B*H*8 floats hold the interval bound)  */
   ICSA_WS_RSTAT,      /* f32 [B*H, NB, 2]   row max and 1 / row sum of the compressed softmax */
   ICSA_WS_COUNT
 };
