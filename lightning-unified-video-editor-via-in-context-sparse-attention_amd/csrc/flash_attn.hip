@@ -50,7 +50,7 @@
 // the fp32 range, and bf16(p) keeps its relative precision at any magnitude.
 #define FA_PSUM_MAX 18446744073709551616.0f
 #ifndef FA_PF
-#define FA_PF 3             // operand prefetch depth (MFMA steps)
+#define FA_PF 5             // operand prefetch depth (MFMA steps); 3, 4, 6 and 8 measured slower
 #endif
 
 __global__ void __launch_bounds__(FA_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
