@@ -75,6 +75,8 @@ enum icsa_ws_slot {
                          (kv_slot order): target blocks, then the selected ones    */
   ICSA_WS_QB,         /* bf16 [B, S, H, D] copy of q (only when q is f32)           */
   ICSA_WS_KB,         /* bf16 [B, S, H, D] copy of k (only when k is f32)           */
+  ICSA_WS_VB,         /* bf16 [B, S, H, D] copy of v (only when v is f32 and
+                         t % 64 != 0: the sparse kernel's row-major values)         */
   ICSA_WS_LOGITS,     /* f32 [B*H, NB, NB]  compressed logits L; the softmax P =
                          exp(L - m) / z with ICSA_WS_RSTAT (P is not stored)        */
   ICSA_WS_OUTC,       /* f32 [B*H, NB, D]   compressed attention output             */
@@ -87,11 +89,7 @@ enum icsa_ws_slot {
   ICSA_WS_KC,         /* bf16 [B*H, NKVp, D]                                        */
   ICSA_WS_VCT,        /* bf16 [B*H, D, NKVp] new-KV block sums of v, transposed (t % 64 == 0 only) */
   ICSA_WS_L3,         /* i32 [B*H, n_diffuse, top_k] per-block exact lists (ascending) */
-  ICSA_WS_KN,         /* bf16 [B*H, Tp, D]  materialised new K (t % 64 != 0 only)    */
-  ICSA_WS_VN,         /* bf16 [B*H, Tp, D]  materialised new V (t % 64 != 0 only)    */
   ICSA_WS_VC,         /* bf16 [B*H, NKVp, D] new-KV block sums of v (t % 64 != 0 only) */
-  ICSA_WS_NKSUM,      /* f32 [B*H, NKV, D]  (t % 64 != 0 only)                       */
-  ICSA_WS_NVSUM,      /* f32 [B*H, NKV, D]  (t % 64 != 0 only)                       */
   ICSA_WS_COLP,       /* f32 [B*H, ceil(n_t/64), n_s] source-column mass per target strip */
   ICSA_WS_L3S,        /* f32 [B*H, n_diffuse, NKV] level-3 block scores (scratch;    */
                       /* afterwards its first B*H*8 floats hold the interval bound)  */
@@ -107,13 +105,14 @@ int icsa_editing_sizes(int B, int S, int H, int D, int t_seq_len, double sparsit
 
 /* Workspace bytes of icsa_editing_sparse_attention for these shapes / dtypes. */
 int64_t icsa_editing_workspace_size(int B, int S, int H, int D, int t_seq_len, double sparsity,
-                                    double srr, double flat_ratio, int q_dtype, int k_dtype);
+                                    double srr, double flat_ratio, int q_dtype, int k_dtype,
+                                    int v_dtype);
 
 /* Byte offsets of every ICSA_WS_* sub-buffer (offsets_out[ICSA_WS_COUNT]; size-0 slots
  * repeat the next offset).  Returns the total size like *_workspace_size. */
 int64_t icsa_editing_workspace_layout(int B, int S, int H, int D, int t_seq_len, double sparsity,
                                       double srr, double flat_ratio, int q_dtype, int k_dtype,
-                                      int64_t* offsets_out);
+                                      int v_dtype, int64_t* offsets_out);
 
 /* The whole in-context sparse attention path for q, k, v [B, S, H, D] (target tokens
  * first, t_seq_len of them): pooling, compressed attention, per-head source retrieval
@@ -309,7 +308,7 @@ int icsa_wan_qk_prologue(
 
 /* icsa_editing_sparse_attention for q / k produced by icsa_wan_qk_prologue: q and k must
  * be bf16, qsum / ksum are their f32 block sums [B*H, NB, D]; stage 1 then pools only v.
- * Workspace: icsa_editing_workspace_size(..., ICSA_BF16, ICSA_BF16).  stage_events as in
+ * Workspace: icsa_editing_workspace_size(..., ICSA_BF16, ICSA_BF16, v_dtype).  stage_events as in
  * icsa_editing_sparse_attention_ev (NULL: none). */
 int icsa_editing_sparse_attention_presummed(
     const void* q, int q_dtype, int64_t q_sb, int64_t q_ss, int64_t q_sh,

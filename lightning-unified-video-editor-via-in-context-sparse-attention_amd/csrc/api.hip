@@ -4,6 +4,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 #include <string>
@@ -84,7 +85,7 @@ struct Layout {
 // then the topK selected source blocks (tile j at columns 64 j .. 64 j + 63)
 int64_t vt_columns(const Sizes& z, int t) { return ((int64_t)ceil_div(t, ICSA_BLOCK) + z.topK) * ICSA_BLOCK; }
 
-Layout editing_layout(int B, int S, int H, const Sizes& z, int t, int q_dtype, int k_dtype) {
+Layout editing_layout(int B, int S, int H, const Sizes& z, int t, int q_dtype, int k_dtype, int v_dtype) {
   const int64_t BH = (int64_t)B * H;
   const int64_t D = ICSA_D;
   const bool unaligned = (t % ICSA_BLOCK) != 0;
@@ -95,6 +96,7 @@ Layout editing_layout(int B, int S, int H, const Sizes& z, int t, int q_dtype, i
   sz[ICSA_WS_VT] = BH * D * vt_columns(z, t) * 2;
   sz[ICSA_WS_QB] = q_dtype == ICSA_F32 ? (int64_t)B * S * H * D * 2 : 0;
   sz[ICSA_WS_KB] = k_dtype == ICSA_F32 ? (int64_t)B * S * H * D * 2 : 0;
+  sz[ICSA_WS_VB] = (unaligned && v_dtype == ICSA_F32) ? (int64_t)B * S * H * D * 2 : 0;
   sz[ICSA_WS_LOGITS] = BH * z.NB * z.NB * 4;
   sz[ICSA_WS_OUTC] = BH * z.NB * D * 4;
   sz[ICSA_WS_SHARP] = BH * z.NB * 4;
@@ -106,12 +108,7 @@ Layout editing_layout(int B, int S, int H, const Sizes& z, int t, int q_dtype, i
   sz[ICSA_WS_KC] = BH * z.NKVp * D * 2;
   sz[ICSA_WS_VCT] = unaligned ? 0 : BH * D * z.NKVp * 2;
   sz[ICSA_WS_L3] = BH * std::max(z.n_diffuse, 1) * z.top_k * 4;
-  const int64_t Tp = z.TKV_pad;
-  sz[ICSA_WS_KN] = unaligned ? BH * Tp * D * 2 : 0;
-  sz[ICSA_WS_VN] = unaligned ? BH * Tp * D * 2 : 0;
   sz[ICSA_WS_VC] = unaligned ? BH * z.NKVp * D * 2 : 0;
-  sz[ICSA_WS_NKSUM] = unaligned ? BH * z.NKV * D * 4 : 0;
-  sz[ICSA_WS_NVSUM] = unaligned ? BH * z.NKV * D * 4 : 0;
   sz[ICSA_WS_COLP] = BH * ceil_div(z.n_t, ICSA_BLOCK) * std::max(z.n_s, 1) * 4;
   sz[ICSA_WS_L3S] = BH * std::max(z.n_diffuse, 1) * z.NKV * 4;
   sz[ICSA_WS_RSTAT] = BH * z.NB * 2 * 4;
@@ -143,6 +140,14 @@ AlphaView make_alpha(const void* alpha, int alpha_dtype, int64_t a_sb, int64_t a
 
 const float kLog2e = 1.4426950408889634f;
 
+// Test hook: ICSA_DEBUG_NO_INTERVAL_SKIP=1 in the environment turns the sparse kernel's
+// interval-bound skip off (interval pass 1 always runs), so that tests can compare the two
+// schedules bit for bit.  Read at every call; no other behaviour depends on the environment.
+bool interval_skip_enabled() {
+  const char* e = std::getenv("ICSA_DEBUG_NO_INTERVAL_SKIP");
+  return !(e != nullptr && e[0] == '1');
+}
+
 }  // namespace
 
 extern "C" {
@@ -166,19 +171,20 @@ int icsa_editing_sizes(int B, int S, int H, int D, int t_seq_len, double sparsit
 
 int64_t icsa_editing_workspace_layout(int B, int S, int H, int D, int t_seq_len, double sparsity,
                                       double srr, double flat_ratio, int q_dtype, int k_dtype,
-                                      int64_t* offsets_out) {
+                                      int v_dtype, int64_t* offsets_out) {
   if (validate_common(B, S, H, D)) return -1;
   if (t_seq_len < 0 || t_seq_len > S) return -1;
   Sizes z = derive(S, t_seq_len, sparsity, srr, flat_ratio);
-  Layout L = editing_layout(B, S, H, z, t_seq_len, q_dtype, k_dtype);
+  Layout L = editing_layout(B, S, H, z, t_seq_len, q_dtype, k_dtype, v_dtype);
   if (offsets_out) std::memcpy(offsets_out, L.off, sizeof(L.off));
   return L.total;
 }
 
 int64_t icsa_editing_workspace_size(int B, int S, int H, int D, int t_seq_len, double sparsity,
-                                    double srr, double flat_ratio, int q_dtype, int k_dtype) {
+                                    double srr, double flat_ratio, int q_dtype, int k_dtype,
+                                    int v_dtype) {
   return icsa_editing_workspace_layout(B, S, H, D, t_seq_len, sparsity, srr, flat_ratio, q_dtype,
-                                       k_dtype, nullptr);
+                                       k_dtype, v_dtype, nullptr);
 }
 
 }  // extern "C"
@@ -230,7 +236,7 @@ int editing_impl(ICSA_EDITING_ARGS, void* const* stage_events, const float* qsum
     return fail(ICSA_EUNSUPPORTED, "NB=%d blocks exceeds the 4096-block limit", z.NB);
   if (z.NKV > 2048 || z.top_k > 512)
     return fail(ICSA_EUNSUPPORTED, "NKV=%d / top_k=%d exceed limits (2048 / 512)", z.NKV, z.top_k);
-  const Layout L = editing_layout(B, S, H, z, t_seq_len, q_dtype, k_dtype);
+  const Layout L = editing_layout(B, S, H, z, t_seq_len, q_dtype, k_dtype, v_dtype);
   if (workspace_bytes < L.total)
     return fail(ICSA_EWORKSPACE, "workspace %lld bytes < required %lld", (long long)workspace_bytes,
                 (long long)L.total);
@@ -253,6 +259,8 @@ int editing_impl(ICSA_EDITING_ARGS, void* const* stage_events, const float* qsum
   pp.sums[2] = reinterpret_cast<float*>(WS(ICSA_WS_VSUM));
   pp.xb[0] = q_dtype == ICSA_F32 ? reinterpret_cast<bf16*>(WS(ICSA_WS_QB)) : nullptr;
   pp.xb[1] = k_dtype == ICSA_F32 ? reinterpret_cast<bf16*>(WS(ICSA_WS_KB)) : nullptr;
+  // row-major bf16 values for the sparse kernel's straddling tiles (t % 64 != 0)
+  pp.xb[2] = (unaligned && v_dtype == ICSA_F32) ? reinterpret_cast<bf16*>(WS(ICSA_WS_VB)) : nullptr;
   pp.xb_sb = (int64_t)S * H * ICSA_D; pp.xb_ss = (int64_t)H * ICSA_D; pp.xb_sh = ICSA_D;
   pp.vt = reinterpret_cast<bf16*>(WS(ICSA_WS_VT));
   pp.vt_sb = (int64_t)H * ICSA_D * Tvt; pp.vt_sh = ICSA_D * Tvt; pp.vt_sd = Tvt;
@@ -303,56 +311,34 @@ int editing_impl(ICSA_EDITING_ARGS, void* const* stage_events, const float* qsum
   sp.sel = sel; sp.order = order;
   sp.kvmap = reinterpret_cast<int*>(WS(ICSA_WS_KVMAP));
   sp.BH = BH; sp.NB = z.NB; sp.n_t = z.n_t; sp.n_s = z.n_s; sp.topK = z.topK; sp.NKV = z.NKV;
-  sp.materialized = unaligned ? 1 : 0;
   sp.inject_sel = inject_sel ? 1 : 0;
   sp.inject_order = inject_order ? 1 : 0;
   ICSA_HIP_TRY(launch_select(sp, stream), "select");
   ICSA_HIP_TRY(launch_vt_blocks(pp, sel, z.n_t, std::max(z.topK, 1), z.topK, pp.vt_nblk, stream),
                "V^T of the selected blocks");
 
-  // ---- new-KV block sums (in place for aligned t, materialised otherwise) ----
+  // ---- new-KV block sums ----
+  // The new KV is read in place.  For t % 64 != 0 its blocks from n_t on straddle two
+  // blocks of the sequence (the t % 64 target-tail tokens, or the tail of the previous
+  // selected block, then the head of the next one); their sums come from the token rows.
+  const int seg_a = t_seq_len % ICSA_BLOCK;
   NewKvSumsParams np;
+  std::memset(&np, 0, sizeof(np));
   np.kc32 = reinterpret_cast<float*>(WS(ICSA_WS_KC32));
   np.kc = reinterpret_cast<bf16*>(WS(ICSA_WS_KC));
   np.vct = unaligned ? nullptr : reinterpret_cast<bf16*>(WS(ICSA_WS_VCT));
   np.vc = unaligned ? reinterpret_cast<bf16*>(WS(ICSA_WS_VC)) : nullptr;
   np.BH = BH; np.NKV = z.NKV; np.NKVp = z.NKVp;
-  const bf16* sk_k;            // key source of the sparse kernel
-  int64_t sk_sb, sk_st, sk_sh;
-  const bf16* sk_v;             // values of the sparse kernel: V^T (aligned) or rows
-  int64_t sk_vs0, sk_vs1, sk_vs2;
-  int sk_Sk;
-  if (!unaligned) {
-    np.ksum = ksum; np.vsum = pp.sums[2];
-    np.kvmap = sp.kvmap; np.map_identity = 0; np.Nsrc = z.NB;
-    sk_k = kb; sk_sb = kb_sb; sk_st = kb_ss; sk_sh = kb_sh;
-    sk_v = pp.vt; sk_vs0 = pp.vt_sb; sk_vs1 = pp.vt_sh; sk_vs2 = pp.vt_sd;
-    sk_Sk = S;
-  } else {
-    const int64_t Tp = z.TKV_pad;
-    GatherParams gp;
-    gp.k = TokTensor{k, k_sb, k_ss, k_sh, k_dtype};
-    gp.v = TokTensor{v, v_sb, v_ss, v_sh, v_dtype};
-    gp.sel = sel;
-    gp.kn = reinterpret_cast<bf16*>(WS(ICSA_WS_KN));
-    gp.vn = reinterpret_cast<bf16*>(WS(ICSA_WS_VN));
-    gp.B = B; gp.H = H; gp.S = S; gp.t = t_seq_len; gp.topK = z.topK; gp.Tkv = z.Tkv; gp.Tp = (int)Tp;
-    ICSA_HIP_TRY(launch_gather(gp, stream), "gather new KV");
-    PoolParams pn;
-    std::memset(&pn, 0, sizeof(pn));
-    // materialised [B*H, Tp, D] viewed as [B, Tp, H, D]-strided tensors
-    pn.x[1] = TokTensor{gp.kn, (int64_t)H * Tp * ICSA_D, ICSA_D, Tp * ICSA_D, ICSA_BF16};
-    pn.x[2] = TokTensor{gp.vn, (int64_t)H * Tp * ICSA_D, ICSA_D, Tp * ICSA_D, ICSA_BF16};
-    pn.sums[1] = reinterpret_cast<float*>(WS(ICSA_WS_NKSUM));
-    pn.sums[2] = reinterpret_cast<float*>(WS(ICSA_WS_NVSUM));
-    pn.B = B; pn.S = (int)Tp; pn.H = H; pn.NB = z.NKV;
-    ICSA_HIP_TRY(launch_pool(pn, stream), "pool new KV");
-    np.ksum = pn.sums[1]; np.vsum = pn.sums[2];
-    np.kvmap = nullptr; np.map_identity = 1; np.Nsrc = z.NKV;
-    sk_k = gp.kn; sk_sb = (int64_t)H * Tp * ICSA_D; sk_st = ICSA_D; sk_sh = Tp * ICSA_D;
-    sk_v = gp.vn; sk_vs0 = (int64_t)H * Tp * ICSA_D; sk_vs1 = ICSA_D; sk_vs2 = Tp * ICSA_D;   // rows
-    sk_Sk = (int)Tp;
-  }
+  np.ksum = ksum; np.vsum = pp.sums[2];
+  np.kvmap = sp.kvmap; np.map_identity = 0; np.Nsrc = z.NB;
+  np.k = TokTensor{k, k_sb, k_ss, k_sh, k_dtype};
+  np.v = TokTensor{v, v_sb, v_ss, v_sh, v_dtype};
+  np.seg_a = seg_a; np.seg_from = z.n_t; np.S = S; np.H = H;
+  // values of the sparse kernel: V^T tiles (aligned t) or row-major bf16 rows (straddling tiles)
+  const bf16* vrow = v_dtype == ICSA_BF16 ? reinterpret_cast<const bf16*>(v) : pp.xb[2];
+  const int64_t vr_sb = v_dtype == ICSA_BF16 ? v_sb : pp.xb_sb;
+  const int64_t vr_ss = v_dtype == ICSA_BF16 ? v_ss : pp.xb_ss;
+  const int64_t vr_sh = v_dtype == ICSA_BF16 ? v_sh : pp.xb_sh;
   if (z.n_diffuse > 0) ICSA_HIP_TRY(launch_newkv_sums(np, stream), "new-KV sums");
 
   // ---- level-3 selection for the diffuse blocks ----
@@ -378,19 +364,19 @@ int editing_impl(ICSA_EDITING_ARGS, void* const* stage_events, const float* qsum
   // ---- stage 4: sparse piecewise attention on the diffuse blocks ----
   if (z.n_diffuse > 0) {
     SparseParams s;
+    std::memset(&s, 0, sizeof(s));
     s.q = qb; s.q_sb = qb_sb; s.q_ss = qb_ss; s.q_sh = qb_sh;
-    s.k = sk_k; s.k_sb = sk_sb; s.k_st = sk_st; s.k_sh = sk_sh;
+    s.k = kb; s.k_sb = kb_sb; s.k_st = kb_ss; s.k_sh = kb_sh;
     s.v_rows = unaligned ? 1 : 0;
     if (unaligned) {
-      s.v = sk_v; s.v_sb = sk_vs0; s.v_st = sk_vs1; s.v_sh = sk_vs2;
-      s.vt = nullptr; s.vt_sb = s.vt_sh = s.vt_sd = 0;
+      s.v = vrow; s.v_sb = vr_sb; s.v_st = vr_ss; s.v_sh = vr_sh;
     } else {
-      s.vt = sk_v; s.vt_sb = sk_vs0; s.vt_sh = sk_vs1; s.vt_sd = sk_vs2;
-      s.v = nullptr; s.v_sb = s.v_st = s.v_sh = 0;
+      s.vt = pp.vt; s.vt_sb = pp.vt_sb; s.vt_sh = pp.vt_sh; s.vt_sd = pp.vt_sd;
     }
-    s.B = B; s.H = H; s.Sq = S; s.Sk = sk_Sk;
+    s.B = B; s.H = H; s.Sq = S; s.Sk = S;
     s.qblocks = order; s.qb_offset = z.n_peaked; s.qb_stride = z.NB; s.n_qblk = z.n_diffuse;
-    s.kvmap = sp.kvmap; s.kvmap_identity = unaligned ? 1 : 0;
+    s.kvmap = sp.kvmap; s.kvmap_identity = 0;
+    s.seg_a = seg_a; s.seg_from = z.n_t;
     s.idx = l3; s.top_k = z.top_k; s.NKV = z.NKV; s.NKVp = z.NKVp;
     s.kc = np.kc; s.vct = np.vct; s.vc = np.vc;
     s.out_c = cp.out_c; s.nb_q = z.NB;
@@ -398,9 +384,11 @@ int editing_impl(ICSA_EDITING_ARGS, void* const* stage_events, const float* qsum
     s.mask_tail = 0;                   // zero-padded new KV attended with logit 0 (TileLang)
     // the level-3 score rows are free again: BH * min(8, cdiv(NKV, 16)) floats of them hold the |KC_j|
     // bound of the interval pass
-    s.kc_bound = reinterpret_cast<float*>(WS(ICSA_WS_L3S));
-    ICSA_HIP_TRY(launch_kc_bound(np.kc, BH, z.NKV, z.NKVp, reinterpret_cast<float*>(WS(ICSA_WS_L3S)),
-                                 &s.kc_bound_n, stream), "interval bound");
+    if (interval_skip_enabled()) {
+      s.kc_bound = reinterpret_cast<float*>(WS(ICSA_WS_L3S));
+      ICSA_HIP_TRY(launch_kc_bound(np.kc, BH, z.NKV, z.NKVp, reinterpret_cast<float*>(WS(ICSA_WS_L3S)),
+                                   &s.kc_bound_n, stream), "interval bound");
+    }
     ICSA_HIP_TRY(launch_sparse(s, stream), "sparse attention");
   }
   ICSA_HIP_TRY(mark(ICSA_STAGE_SPARSE), "event");
@@ -457,11 +445,19 @@ constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 void* g_scratch_dev[kMaxDevices] = {};
 
-// Device address of `scratch` on the current device, looked up on the first call made
-// with that device current and kept for later calls.
-int scratch_for_current_device(void** out) {
-  int dev = 0;
+// Device address of `scratch` on the device that runs `stream`, looked up on the first
+// call for that device and kept for later calls.  The lookup needs that device current,
+// and the launches that follow set per-device kernel attributes on the current device,
+// so a stream of any other device is refused.
+int scratch_for_stream_device(hipStream_t stream, void** out) {
+  int dev = 0, sdev = 0;
   ICSA_HIP_TRY(hipGetDevice(&dev), "hipGetDevice");
+  if (stream != nullptr) {
+    ICSA_HIP_TRY(hipStreamGetDevice(stream, &sdev), "hipStreamGetDevice");
+    if (sdev != dev)
+      return fail(ICSA_EINVAL, "stream belongs to device %d but device %d is current; make the "
+                  "stream's device current before the call", sdev, dev);
+  }
   if (dev < 0 || dev >= kMaxDevices)
     return fail(ICSA_EUNSUPPORTED, "device %d outside the %d devices the scratch table covers", dev, kMaxDevices);
   std::lock_guard<std::mutex> lock(g_scratch_mu);
@@ -492,17 +488,18 @@ int icsa_editing_sparse_attention_noalloc(
   // sizes first: an oversized request fails before any HIP call
   int rc = validate_common(B, S, H, D);
   if (rc) return rc;
-  if ((rc = check_dtype(q_dtype, "q")) || (rc = check_dtype(k_dtype, "k"))) return rc;
+  if ((rc = check_dtype(q_dtype, "q")) || (rc = check_dtype(k_dtype, "k")) || (rc = check_dtype(v_dtype, "v")))
+    return rc;
   if (t_seq_len < 0 || t_seq_len > S) return fail(ICSA_EINVAL, "t_seq_len %d outside [0, S=%d]", t_seq_len, S);
   const Sizes z = derive(S, t_seq_len, sparsity, srr, flat_ratio);
-  const int64_t need = editing_layout(B, S, H, z, t_seq_len, q_dtype, k_dtype).total;
+  const int64_t need = editing_layout(B, S, H, z, t_seq_len, q_dtype, k_dtype, v_dtype).total;
   if (need > (int64_t)ICSA_NOALLOC_SCRATCH_BYTES)
     return fail(ICSA_EUNSUPPORTED,
                 "this call needs %lld bytes of scratch, more than the %lld-byte static scratch of "
                 "icsa_editing_sparse_attention_noalloc; call icsa_editing_sparse_attention with a "
                 "workspace instead", (long long)need, (long long)ICSA_NOALLOC_SCRATCH_BYTES);
   void* ws = nullptr;
-  if ((rc = scratch_for_current_device(&ws))) return rc;
+  if ((rc = scratch_for_stream_device(reinterpret_cast<hipStream_t>(stream_), &ws))) return rc;
   void* workspace = ws;
   const int64_t workspace_bytes = ICSA_NOALLOC_SCRATCH_BYTES;
   return editing_impl(ICSA_EDITING_PASS, nullptr, nullptr, nullptr);
@@ -703,6 +700,7 @@ static int sparse_piecewise_impl(
   ICSA_HIP_TRY(launch_pool(pk, stream), "pool k/v");
 
   NewKvSumsParams np;
+  std::memset(&np, 0, sizeof(np));  // seg_a = 0: no straddling blocks
   np.ksum = pk.sums[1]; np.vsum = pk.sums[2]; np.kvmap = nullptr; np.map_identity = 1;
   np.kc32 = reinterpret_cast<float*>(ws + L.kc32);
   np.kc = reinterpret_cast<bf16*>(ws + L.kc);
@@ -727,6 +725,7 @@ static int sparse_piecewise_impl(
                  "copy idx");
 
   SparseParams s;
+  std::memset(&s, 0, sizeof(s));   // seg_a = 0: the caller's new KV is contiguous
   s.q = reinterpret_cast<const bf16*>(q); s.q_sb = q_sb; s.q_ss = q_st; s.q_sh = q_sh;
   s.k = reinterpret_cast<const bf16*>(k); s.k_sb = k_sb; s.k_st = k_st; s.k_sh = k_sh;
   s.v_rows = 1;                      // v read in place, row tiles
@@ -745,9 +744,11 @@ static int sparse_piecewise_impl(
   s.mask_tail = triton;
   // the block top-k score rows are free again: BH * min(8, cdiv(NKV, 16)) floats of them hold the
   // |KC_j| bound of the interval pass
-  s.kc_bound = reinterpret_cast<float*>(ws + L.scores);
-  ICSA_HIP_TRY(launch_kc_bound(np.kc, BH, NKV, NKVp, reinterpret_cast<float*>(ws + L.scores),
-                               &s.kc_bound_n, stream), "interval bound");
+  if (interval_skip_enabled()) {
+    s.kc_bound = reinterpret_cast<float*>(ws + L.scores);
+    ICSA_HIP_TRY(launch_kc_bound(np.kc, BH, NKV, NKVp, reinterpret_cast<float*>(ws + L.scores),
+                                 &s.kc_bound_n, stream), "interval bound");
+  }
   ICSA_HIP_TRY(launch_sparse(s, stream), "sparse attention");
   return ICSA_OK;
 }

@@ -488,11 +488,11 @@ __global__ void __launch_bounds__(1024) icsa_select_kernel(SelectParams p) {
   }
   __syncthreads();
   // new-KV block j -> source block: target blocks, then the selected source blocks in
-  // ranked order, then zero padding (-1).
+  // ranked order, then zero padding (-1).  With t % 64 != 0 the blocks from n_t on straddle
+  // two of these (the kernels take the first t % 64 rows from the block before).
   for (int j = threadIdx.x; j < p.NKV; j += blockDim.x) {
     int src;
-    if (p.materialized) src = j;
-    else if (j < n_t) src = j;
+    if (j < n_t) src = j;
     else if (j < n_t + p.topK) src = n_t + sel_l[j - n_t];
     else src = -1;
     p.kvmap[(int64_t)bh * p.NKV + j] = src;
@@ -510,6 +510,7 @@ hipError_t launch_select(const SelectParams& p, hipStream_t stream) {
 // ---------------------------------------------------------------------------------------
 __global__ void __launch_bounds__(128) icsa_newkv_sums_kernel(NewKvSumsParams p) {
   const int j = blockIdx.x, bh = blockIdx.y, d = threadIdx.x;
+  if (p.seg_a > 0 && j >= p.seg_from && j < p.NKV) return;   // icsa_newkv_straddle_kernel
   int src = -1;
   if (j < p.NKV) src = p.map_identity ? j : p.kvmap[(int64_t)bh * p.NKV + j];
   float ks = 0.f, vs = 0.f;
@@ -523,8 +524,65 @@ __global__ void __launch_bounds__(128) icsa_newkv_sums_kernel(NewKvSumsParams p)
   if (p.vc) p.vc[((int64_t)bh * p.NKVp + j) * ICSA_D + d] = f2bf(vs);
 }
 
+// Straddling new-KV block j (the pipeline's new KV when t % 64 != 0; see SparseParams):
+// rows r < a from tokens segA + r, rows r >= a from 64 kvmap[j] + r - a, summed straight
+// from the token rows.  Thread t: 8 dims 8 (t % 16) .. + 7 of rows t / 16 + 8 m; the 8
+// row groups are added in fixed order.
+template <typename TK, typename TV>
+__global__ void __launch_bounds__(128) icsa_newkv_straddle_kernel(NewKvSumsParams p) {
+  __shared__ float red[2][8][ICSA_D + 4];
+  const int j = p.seg_from + blockIdx.x, bh = blockIdx.y;
+  const int b = bh / p.H, h = bh % p.H;
+  const int t = threadIdx.x, c = t & 15, g = t >> 4;
+  const int a = p.seg_a;
+  const int* map = p.kvmap + (int64_t)bh * p.NKV;
+  int tokA = -1;
+  if (j == p.seg_from) tokA = ICSA_BLOCK * p.seg_from;
+  else if (map[j - 1] >= 0) tokA = ICSA_BLOCK * map[j - 1] + ICSA_BLOCK - a;
+  const int tokB = map[j] >= 0 ? ICSA_BLOCK * map[j] - a : -1;    // token of row r >= a: tokB + r
+  const TK* kb = reinterpret_cast<const TK*>(p.k.p) + (int64_t)b * p.k.sb + (int64_t)h * p.k.sh;
+  const TV* vb = reinterpret_cast<const TV*>(p.v.p) + (int64_t)b * p.v.sb + (int64_t)h * p.v.sh;
+  float ks[8], vs[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) { ks[e] = 0.f; vs[e] = 0.f; }
+#pragma unroll
+  for (int m = 0; m < 8; ++m) {
+    const int r = g + 8 * m;
+    const int tok = r < a ? (tokA < 0 ? -1 : tokA + r) : (tokB < 0 ? -1 : tokB + r);
+    if (tok >= 0 && tok < p.S) {
+      float x[8];
+      load8_f32(kb + (int64_t)tok * p.k.ss + 8 * c, x);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ks[e] += x[e];
+      load8_f32(vb + (int64_t)tok * p.v.ss + 8 * c, x);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) vs[e] += x[e];
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) { red[0][g][8 * c + e] = ks[e]; red[1][g][8 * c + e] = vs[e]; }
+  __syncthreads();
+  const int d = t;
+  float k_sum = 0.f, v_sum = 0.f;
+#pragma unroll
+  for (int gg = 0; gg < 8; ++gg) { k_sum += red[0][gg][d]; v_sum += red[1][gg][d]; }
+  p.kc32[((int64_t)bh * p.NKV + j) * ICSA_D + d] = k_sum;
+  p.kc[((int64_t)bh * p.NKVp + j) * ICSA_D + d] = f2bf(k_sum);
+  if (p.vct) p.vct[((int64_t)bh * ICSA_D + d) * p.NKVp + (j & ~15) + kv_slot(j & 15)] = f2bf(v_sum);
+  if (p.vc) p.vc[((int64_t)bh * p.NKVp + j) * ICSA_D + d] = f2bf(v_sum);
+}
+
 hipError_t launch_newkv_sums(const NewKvSumsParams& p, hipStream_t stream) {
   hipLaunchKernelGGL(icsa_newkv_sums_kernel, dim3(p.NKVp, p.BH), dim3(128), 0, stream, p);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || p.seg_a <= 0 || p.seg_from >= p.NKV) return e;
+  if (!p.kvmap || !p.k.p || !p.v.p) return hipErrorInvalidValue;
+  const dim3 grid(p.NKV - p.seg_from, p.BH);
+  const bool kf = p.k.dtype == ICSA_DT_F32, vf = p.v.dtype == ICSA_DT_F32;
+  if (kf && vf) hipLaunchKernelGGL((icsa_newkv_straddle_kernel<float, float>), grid, dim3(128), 0, stream, p);
+  else if (kf) hipLaunchKernelGGL((icsa_newkv_straddle_kernel<float, bf16>), grid, dim3(128), 0, stream, p);
+  else if (vf) hipLaunchKernelGGL((icsa_newkv_straddle_kernel<bf16, float>), grid, dim3(128), 0, stream, p);
+  else hipLaunchKernelGGL((icsa_newkv_straddle_kernel<bf16, bf16>), grid, dim3(128), 0, stream, p);
   return hipGetLastError();
 }
 

@@ -46,7 +46,6 @@ struct SelectParams {
   int* order;           // [BH, NB]     (first n_peaked peaked, rest diffuse)
   int* kvmap;           // [BH, NKV]    start block in the K/Vt source of new-KV block j, -1 zero
   int BH, NB, n_t, n_s, topK, NKV;
-  int materialized;     // 1: new KV materialised in its own buffers (kvmap = identity)
   int inject_sel, inject_order;   // 1: sel / order already hold caller decisions
 };
 hipError_t launch_select(const SelectParams& p, hipStream_t stream);
@@ -61,6 +60,10 @@ struct NewKvSumsParams {
   bf16* vct;            // [BH, D, NKVp]  bf16 sums of v transposed, kv_slot() order (nullptr: none)
   bf16* vc;             // [BH, NKVp, D]  bf16 sums of v, row-major (nullptr: none)
   int BH, Nsrc, NKV, NKVp;
+  // straddling blocks j in [seg_from, NKV) (seg_a > 0; see SparseParams) are summed from the
+  // token rows of k / v (dtype as given, rows >= S zero) instead of copied from ksum / vsum
+  TokTensor k, v;
+  int seg_a, seg_from, S, H;
 };
 hipError_t launch_newkv_sums(const NewKvSumsParams& p, hipStream_t stream);
 
@@ -156,6 +159,12 @@ struct SparseParams {
                                      // attended with logit 0 (TileLang's zero padding)
   const int* qblocks; int qb_offset, qb_stride; int n_qblk;
   const int* kvmap; int kvmap_identity;         // [BH, NKV] source block of new-KV block
+  // Straddling new-KV blocks (the pipeline's in-place new KV when t % 64 != 0): block
+  // j >= seg_from takes rows r < seg_a from tokens segA(j) + r and rows r >= seg_a from
+  // 64 kvmap[j] + r - seg_a, with segA(seg_from) = 64 seg_from (the target tail) and
+  // segA(j) = 64 kvmap[j - 1] + 64 - seg_a otherwise (the tail of the previous selected
+  // block).  seg_a = 0: every block is the 64 rows from 64 kvmap[j].  Row-major V only.
+  int seg_a, seg_from;
   const int* idx;                    // [BH, n_qblk, top_k] ascending
   int top_k, NKV, NKVp;
   const bf16* kc;                    // [BH, NKVp, D]

@@ -163,6 +163,7 @@ hipError_t launch_pool(const PoolParams& p, hipStream_t stream) {
 }
 
 // V^T of listed blocks: one workgroup per (b*h, list entry r), stored as V^T block dst0 + r
+// (an entry outside [0, NB) stores a zero block, so no column keeps stale workspace data)
 template <typename T>
 __global__ void __launch_bounds__(256) icsa_vt_blocks_kernel(PoolParams p, const int* list, int base,
                                                              int stride, int dst0) {
@@ -170,9 +171,14 @@ __global__ void __launch_bounds__(256) icsa_vt_blocks_kernel(PoolParams p, const
   const int bh = blockIdx.x, r = blockIdx.y;
   const int b = bh / p.H, h = bh % p.H;
   const int n = base + list[(int64_t)bh * stride + r];
-  if (n < 0 || n >= p.NB) return;                  // uniform for the workgroup
+  const bool real = n >= 0 && n < p.NB;            // uniform for the workgroup
   Raw8<T> rows[4];
-  pool_load<T>(p, p.vt_src, n, b, h, rows);
+  if (real) {
+    pool_load<T>(p, p.vt_src, n, b, h, rows);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) rows[j].zero();
+  }
   const int c = threadIdx.x & 15, g = threadIdx.x >> 4;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {

@@ -26,7 +26,11 @@
 // The new KV is read in place: new-KV block j lives at source block kvmap[j] of the
 // K / V buffers -- target blocks and the selected source blocks of the original
 // sequence -- or is an all-zero block (kvmap -1 / an out-of-range caller index, the
-// reference's TKV zero padding, attended with logit 0).  KC and VC (or VC^T) are the bf16
+// reference's TKV zero padding, attended with logit 0).  When t % 64 != 0 the new-KV
+// blocks from n_t on straddle two of those (the reference concatenates t target tokens
+// with whole 64-token source blocks, editing_sparse_attention.py:138-159): the first
+// t % 64 rows come from the tail of the block before, the rest from the head of
+// kvmap[j], and each lane's DMA row picks its segment (SparseParams::seg_a).  KC and VC (or VC^T) are the bf16
 // block sums of the new KV.  With mask_tail (the Triton host's ragged TKV)
 // the keys of an exact block at or past Sk get no weight instead (triton_kernels.py:185);
 // the interval part is the same in both modes.
@@ -34,7 +38,8 @@
 // Workgroup = 2 waves = one query block (wave w: rows 32 w .. 32 w + 31); four workgroups
 // share a CU.  One K buffer and one V buffer per workgroup, filled by direct
 // global->LDS loads (lane l lands at M0 + 16 l; the XOR swizzle is applied on the global
-// side).  V comes in one of two layouts (template parameter VROW):
+// side).  V comes in one of two layouts (template parameter VROW; SEG adds the straddling
+// new-KV blocks, row-major V only):
 //   * VROW: 64 rows of the caller's row-major V, a row tile (attn_tile.h) whose PV
 //     operands are formed by transposing LDS reads -- no transposed copy of V is needed
 //     (the sparse host entry points, and the materialised new KV of t % 64 != 0);
@@ -70,7 +75,13 @@
 #define SP_WAIT_OLDER() asm volatile("s_waitcnt vmcnt(8)" ::: "memory")
 #define SP_WAIT_ALL() asm volatile("s_waitcnt vmcnt(0)" ::: "memory")
 
-template <bool VROW>
+// Real rows of a loaded tile: [0, vA) of the first segment [0, a) and [a, a + vB) of the
+// second; every other row is zeroed after the load (a = 0: rows [0, vB) real).
+struct TileRows {
+  int a, vA, vB;
+};
+
+template <bool VROW, bool SEG>
 __global__ void __launch_bounds__(SP_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
 icsa_sparse_kernel(SparseParams p) {
   // K tile and V tile as separate objects, so the compiler can tell a load into one from
@@ -78,6 +89,7 @@ icsa_sparse_kernel(SparseParams p) {
   __shared__ __attribute__((aligned(16))) unsigned char kbuf[SP_BUF_BYTES];
   __shared__ __attribute__((aligned(16))) unsigned char vbuf[SP_BUF_BYTES];
   __shared__ int src_l[SP_MAX_TOPK];                  // source block of exact tile t (-1: zeros)
+  __shared__ int tokA_l[SP_MAX_TOPK];                 // straddling tile: token of row 0 (-1: none)
   __shared__ int nkv_l[SP_MAX_TOPK];                  // its new-KV block (V^T column block; -1: zeros)
   __shared__ unsigned long long sel_l[SP_MAX_CHUNKS];  // selected new-KV blocks per chunk
   __shared__ int rot_l;                               // exact tiles visited from list entry rot_l
@@ -114,12 +126,19 @@ icsa_sparse_kernel(SparseParams p) {
     for (int t = tid; t < top_k; t += SP_THREADS) {
       const int j = idx_g[t];
       int src = -1;                 // out-of-range entries of a caller list: a zero block
+      int tok_a = -1;
       if (j >= 0 && j < p.NKV) {
         src = p.kvmap_identity ? j : kvmap[j];
+        if (SEG && j >= p.seg_from) {
+          const int prev = j == p.seg_from ? -2 : (p.kvmap_identity ? j - 1 : kvmap[j - 1]);
+          tok_a = prev == -2 ? ATT_BN * p.seg_from
+                             : (prev >= 0 ? ATT_BN * prev + ATT_BN - p.seg_a : 0x3fffffff);  // past Sk: zeros
+        }
         atomicOr(&sel_l[j >> 6], 1ull << (j & 63));
         if (j < sweep0) atomicAdd(&rot_l, 1);
       }
       src_l[t] = src;
+      tokA_l[t] = tok_a;
       nkv_l[t] = src >= 0 ? j : -1;
     }
   }
@@ -162,17 +181,47 @@ icsa_sparse_kernel(SparseParams p) {
   // list entry of exact tile g (the ascending list rotated to start at entry rot)
   auto ex_entry = [&](int g) -> int { return g + rot < top_k ? g + rot : g + rot - top_k; };
 
+  // A straddling exact tile (tokA_l >= 0): rows r < seg_a from token tok_a + r, rows
+  // r >= seg_a from token 64 src + r - seg_a.  One buffer resource over the head's rows,
+  // per-lane row offsets; rows past Sk (or of a zero block) read token 0 and are zeroed
+  // after the wait.  Returns the rows that are real: [0, vA) and [seg_a, seg_a + vB).
+  const int seg_a = p.seg_a;
+  auto issue_straddle = [&](unsigned char* dst, const bf16* head, int64_t rs_el, int tok_a, int src,
+                            bool vrow) -> TileRows {
+    const int tok_b = src < 0 ? -1 : ATT_BN * src;
+    TileRows v;
+    v.a = seg_a;
+    v.vA = max(0, min(seg_a, p.Sk - tok_a));
+    v.vB = tok_b < 0 ? 0 : max(0, min(ATT_BN - seg_a, p.Sk - tok_b));
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(head, ((int64_t)(p.Sk - 1) * rs_el + ICSA_D) * 2);
+    const int rs2 = (int)rs_el * 2;
+#pragma unroll
+    for (int i = 0; i < SP_DMA_PER_TILE; ++i) {
+      const int r = k_row0 + 4 * i;
+      const bool lo = r < seg_a;
+      const bool ok = lo ? r < v.vA : r - seg_a < v.vB;
+      const int tok = ok ? (lo ? tok_a + r : tok_b + r - seg_a) : 0;
+      const int swz = vrow ? rv_swz(r) : (r & 15);
+      const int off = tok * rs2 + (((lane & 15) ^ swz) << 4);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)(dst + 1024 * i), 16, off, 0, 0, 0);
+    }
+    return v;
+  };
+
   // Tile g: g < T1 exact block src_l[g]; T1 <= g < T2 pass-1 chunk g - T1 (K only);
-  // g >= T2 pass-2 chunk g - T2.  issue_k / issue_v return the number of real keys (the
+  // g >= T2 pass-2 chunk g - T2.  issue_k / issue_v return the rows that are real (the
   // rest are zeroed after the wait; a V^T tile is either all real -- the copy is zero
   // padded -- or a zero block).
-  auto issue_k = [&](int g) -> int {
+  auto issue_k = [&](int g) -> TileRows {
     const bf16* base;
     int64_t bytes;
     int valid, rs2;                        // rs2: key row stride in bytes
     const bool ex = g < T1;
     if (ex) {
+      const int tok_a = __builtin_amdgcn_readfirstlane(tokA_l[ex_entry(g)]);
       const int src = __builtin_amdgcn_readfirstlane(src_l[ex_entry(g)]);
+      if constexpr (SEG)
+        if (tok_a >= 0) return issue_straddle(kbuf + wave * 8192, kbase, p.k_st, tok_a, src, false);
       const int tok0 = src * ATT_BN;
       valid = src < 0 ? 0 : min(ATT_BN, p.Sk - tok0);
       base = kbase + (src < 0 ? 0 : (int64_t)tok0 * p.k_st);
@@ -193,9 +242,9 @@ icsa_sparse_kernel(SparseParams p) {
       const int off = r * rs2 + (((lane & 15) ^ (r & 15)) << 4);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)(dst + 1024 * i), 16, off, 0, 0, 0);
     }
-    return valid;
+    return TileRows{0, 0, valid};
   };
-  auto issue_v = [&](int g) -> int {
+  auto issue_v = [&](int g) -> TileRows {
     const bf16* base;
     int64_t bytes;
     int valid, rs2;                        // rs2: row stride in bytes (V rows / V^T d rows)
@@ -204,6 +253,9 @@ icsa_sparse_kernel(SparseParams p) {
       const int src = __builtin_amdgcn_readfirstlane(src_l[ex_entry(g)]);
       const int tok0 = src * ATT_BN;
       if constexpr (VROW) {
+        const int tok_a = __builtin_amdgcn_readfirstlane(tokA_l[ex_entry(g)]);
+        if constexpr (SEG)
+          if (tok_a >= 0) return issue_straddle(vbuf + wave * 8192, vbase, p.v_st, tok_a, src, true);
         valid = src < 0 ? 0 : min(ATT_BN, p.Sk - tok0);
         base = vbase + (src < 0 ? 0 : (int64_t)tok0 * p.v_st);
         bytes = valid > 0 ? ((int64_t)(valid - 1) * p.v_st + ICSA_D) * 2 : 0;
@@ -236,25 +288,25 @@ icsa_sparse_kernel(SparseParams p) {
       }
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)(dst + 1024 * i), 16, off, 0, 0, 0);
     }
-    return valid;
+    return TileRows{0, 0, valid};
   };
-  // After the wait: zero this wave's key rows >= valid of the K buffer / a V row tile
-  // (rows past the sequence and zero blocks are zero keys and values).
-  auto fill_rows = [&](unsigned char* buf, int valid) {
-    if (valid >= ATT_BN) return;
+  // After the wait: zero this wave's key rows that are not real in the K buffer / a V row
+  // tile (rows past the sequence and zero blocks are zero keys and values).
+  auto fill_rows = [&](unsigned char* buf, TileRows v) {
+    if (v.vA >= v.a && v.vB >= ATT_BN - v.a) return;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int r = 32 * wave + 4 * i + (lane >> 4);
-      if (r >= valid)                      // 4-byte stores: one zero register
+      if (r < v.a ? r >= v.vA : r - v.a >= v.vB)   // 4-byte stores: one zero register
         for (int e = 0; e < 4; ++e) *reinterpret_cast<unsigned*>(buf + r * ICSA_D * 2 + (lane & 15) * 16 + 4 * e) = 0u;
     }
   };
   // ... and this wave's half of a V^T tile of a zero block
-  auto fill_v = [&](int valid) {
+  auto fill_v = [&](TileRows v) {
     if constexpr (VROW) {
-      fill_rows(vbuf, valid);
+      fill_rows(vbuf, v);
     } else {
-      if (valid > 0) return;
+      if (v.vB > 0) return;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const int d = 64 * wave + 8 * i + (lane >> 3);
@@ -348,8 +400,8 @@ icsa_sparse_kernel(SparseParams p) {
   float m_true = -INFINITY;     // exact running max (the reference's m after the exact loop)
   float l_run = 0.f;
 
-  int kv_pending = issue_k(0);
-  int vv_pending = 0;
+  TileRows kv_pending = issue_k(0);
+  TileRows vv_pending{0, 0, 0};
 
   // ---- 1. exact blocks ----
   // Three barriers per block: V(t) is issued right after the first one, which every wave
@@ -361,13 +413,14 @@ icsa_sparse_kernel(SparseParams p) {
     vv_pending = issue_v(t);
     qk();
     ATT_BARRIER();                       // K buffer free
-    const int kv_next = issue_k(t + 1);    // T > T1: always a next K tile
-    if (p.mask_tail && kv_pending < ATT_BN) {  // keys past Sk take no part (Triton host)
+    const TileRows kv_next = issue_k(t + 1);   // T > T1: always a next K tile
+    // keys past Sk take no part (the Triton host; its new KV never straddles)
+    if (p.mask_tail && kv_pending.vB < ATT_BN) {
 #pragma unroll
       for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
         for (int i = 0; i < 16; ++i)
-          if (32 * sub + acc_row(i, lane) >= kv_pending) s[sub][i] = -INFINITY;
+          if (32 * sub + acc_row(i, lane) >= kv_pending.vB) s[sub][i] = -INFINITY;
     }
     float mx = -INFINITY;
 #pragma unroll
@@ -540,9 +593,15 @@ hipError_t launch_sparse(const SparseParams& p, hipStream_t stream) {
   if (p.v_rows ? ((int64_t)p.Sk * p.v_st * 2 > 0x7fffffffLL || 64LL * p.v_st * 2 > 0x7fffffffLL || !p.vc)
                : ((int64_t)ICSA_D * p.vt_sd * 2 > 0x7fffffffLL || !p.vct))
     return hipErrorInvalidValue;
-  if (p.v_rows)
-    hipLaunchKernelGGL(icsa_sparse_kernel<true>, dim3(xcd_grid(n_work)), dim3(SP_THREADS), 0, stream, p);
+  // straddling blocks: row-major V, seg_a in [0, 64), no Triton-style tail mask
+  if (p.seg_a < 0 || p.seg_a >= ATT_BN || (p.seg_a > 0 && (!p.v_rows || p.mask_tail || p.seg_from < 0)))
+    return hipErrorInvalidValue;
+  const dim3 grid(xcd_grid(n_work));
+  if (p.seg_a > 0)
+    hipLaunchKernelGGL((icsa_sparse_kernel<true, true>), grid, dim3(SP_THREADS), 0, stream, p);
+  else if (p.v_rows)
+    hipLaunchKernelGGL((icsa_sparse_kernel<true, false>), grid, dim3(SP_THREADS), 0, stream, p);
   else
-    hipLaunchKernelGGL(icsa_sparse_kernel<false>, dim3(xcd_grid(n_work)), dim3(SP_THREADS), 0, stream, p);
+    hipLaunchKernelGGL((icsa_sparse_kernel<false, false>), grid, dim3(SP_THREADS), 0, stream, p);
   return hipGetLastError();
 }

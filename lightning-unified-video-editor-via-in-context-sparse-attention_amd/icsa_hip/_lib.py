@@ -32,9 +32,8 @@ NOALLOC_SCRATCH_BYTES = 256 << 20
 STAGES = ["start", "pool", "compressed", "select", "sparse", "flash"]
 
 # workspace slots of icsa_editing_sparse_attention (enum icsa_ws_slot)
-WS_SLOTS = ["QSUM", "KSUM", "VSUM", "VT", "QB", "KB", "LOGITS", "OUTC", "SHARP", "SRCSCORE", "SEL",
-            "ORDER", "KVMAP", "KC32", "KC", "VCT", "L3", "KN", "VN", "VC", "NKSUM", "NVSUM",
-            "COLP", "L3S", "RSTAT"]
+WS_SLOTS = ["QSUM", "KSUM", "VSUM", "VT", "QB", "KB", "VB", "LOGITS", "OUTC", "SHARP", "SRCSCORE",
+            "SEL", "ORDER", "KVMAP", "KC32", "KC", "VCT", "L3", "VC", "COLP", "L3S", "RSTAT"]
 
 # every symbol include/icsa.h declares
 EXPORTS = [
@@ -57,8 +56,8 @@ _f = ctypes.c_float
 
 _SIGNATURES = {
     "icsa_editing_sizes": (_i, [_i, _i, _i, _i, _i, _d, _d, _d, _p]),
-    "icsa_editing_workspace_size": (_l, [_i, _i, _i, _i, _i, _d, _d, _d, _i, _i]),
-    "icsa_editing_workspace_layout": (_l, [_i, _i, _i, _i, _i, _d, _d, _d, _i, _i, _p]),
+    "icsa_editing_workspace_size": (_l, [_i, _i, _i, _i, _i, _d, _d, _d, _i, _i, _i]),
+    "icsa_editing_workspace_layout": (_l, [_i, _i, _i, _i, _i, _d, _d, _d, _i, _i, _i, _p]),
     "icsa_editing_sparse_attention": (_i, [
         _p, _i, _l, _l, _l,
         _p, _i, _l, _l, _l,

@@ -94,7 +94,8 @@ def _editing_sparse_attention_hip(q, k, v, t_seq_len, alpha_2=1.0, SPARSITY_RATI
     offs = (ctypes.c_int64 * len(_lib.WS_SLOTS))()
     ws_bytes = L.icsa_editing_workspace_layout(B, S, H, D, t_seq_len, float(SPARSITY_RATIO),
                                                float(srr), float(flat_ratio), dtype_code(q),
-                                               dtype_code(k), ctypes.cast(offs, ctypes.c_void_p))
+                                               dtype_code(k), dtype_code(v),
+                                               ctypes.cast(offs, ctypes.c_void_p))
     if ws_bytes < 0:
         raise _lib.IcsaError("icsa_editing_workspace_layout", int(ws_bytes))
     _require(not noalloc or (not keep_workspace and stage_events is None and presummed is None),
@@ -137,15 +138,16 @@ def _editing_sparse_attention_hip(q, k, v, t_seq_len, alpha_2=1.0, SPARSITY_RATI
     if noalloc:
         fn = L.icsa_editing_sparse_attention_noalloc
         ws_args = []
-    rc = fn(
-        ptr(q), dtype_code(q), q.stride(0), q.stride(1), q.stride(2),
-        ptr(k), dtype_code(k), k.stride(0), k.stride(1), k.stride(2),
-        ptr(v), dtype_code(v), v.stride(0), v.stride(1), v.stride(2),
-        B, S, H, D, int(t_seq_len), float(SPARSITY_RATIO), float(srr), float(flat_ratio),
-        ptr(a), a_dt, a_st[0], a_st[1], a_st[2], a_st[3], float(a_scalar),
-        ptr(out), dtype_code(out), out.stride(0), out.stride(1), out.stride(2),
-        ptr(inj.get("sel")), ptr(inj.get("order")), ptr(inj.get("l3")),
-        *ws_args, stream_ptr(q.device), *ev_args)
+    with torch.cuda.device(q.device):     # the library launches on the current device
+        rc = fn(
+            ptr(q), dtype_code(q), q.stride(0), q.stride(1), q.stride(2),
+            ptr(k), dtype_code(k), k.stride(0), k.stride(1), k.stride(2),
+            ptr(v), dtype_code(v), v.stride(0), v.stride(1), v.stride(2),
+            B, S, H, D, int(t_seq_len), float(SPARSITY_RATIO), float(srr), float(flat_ratio),
+            ptr(a), a_dt, a_st[0], a_st[1], a_st[2], a_st[3], float(a_scalar),
+            ptr(out), dtype_code(out), out.stride(0), out.stride(1), out.stride(2),
+            ptr(inj.get("sel")), ptr(inj.get("order")), ptr(inj.get("l3")),
+            *ws_args, stream_ptr(q.device), *ev_args)
     _lib.check(fn.__name__, rc)
     if not keep_workspace:
         return out, None

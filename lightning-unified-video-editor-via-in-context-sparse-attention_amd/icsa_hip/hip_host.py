@@ -122,14 +122,15 @@ def sparse_piecewise_attn_1st_intervals_hip(q: torch.Tensor, k: torch.Tensor, v:
         _require(tuple(inj.shape) == (B, H, NQ, top_k), f"indices must be [B, H, {NQ}, {top_k}]")
         check_index_lists(inj, NKV, "indices")
     idx_out = torch.empty(B, H, NQ, top_k, dtype=torch.int32, device=q.device) if return_indices else None
-    rc = L.icsa_sparse_piecewise_attn(
-        ptr(q), q.stride(0), q.stride(1), q.stride(2),
-        ptr(k), k.stride(0), k.stride(1), k.stride(2),
-        ptr(v), v.stride(0), v.stride(1), v.stride(2),
-        B, H, TQ, TKV, D, float(sparsity),
-        ptr(inj), ptr(idx_out),
-        ptr(out), out.stride(0), out.stride(1), out.stride(2),
-        ptr(ws), ws_bytes, stream_ptr(q.device))
+    with torch.cuda.device(q.device):     # the library launches on the current device
+        rc = L.icsa_sparse_piecewise_attn(
+            ptr(q), q.stride(0), q.stride(1), q.stride(2),
+            ptr(k), k.stride(0), k.stride(1), k.stride(2),
+            ptr(v), v.stride(0), v.stride(1), v.stride(2),
+            B, H, TQ, TKV, D, float(sparsity),
+            ptr(inj), ptr(idx_out),
+            ptr(out), out.stride(0), out.stride(1), out.stride(2),
+            ptr(ws), ws_bytes, stream_ptr(q.device))
     _lib.check("icsa_sparse_piecewise_attn", rc)
     return (out, idx_out) if return_indices else out
 
@@ -213,14 +214,15 @@ def sparse_piecewise_attn_1st_intervals_fwd_hip(q, k, v, sparsity: float = 0.1, 
         inj = indices.to(device=q.device, dtype=torch.int32).contiguous()
         _require(tuple(inj.shape) == (B, H, NQ, top_k), f"indices must be [B, H, {NQ}, {top_k}]")
         check_index_lists(inj, NKV, "indices")
-    rc = L.icsa_sparse_piecewise_attn_fwd(
-        ptr(q), q.stride(0), q.stride(1), q.stride(2),
-        ptr(k), k.stride(0), k.stride(1), k.stride(2),
-        ptr(v), v.stride(0), v.stride(1), v.stride(2),
-        B, H, TQ, TKV, D, float(sparsity),
-        ptr(inj), ptr(idx),
-        ptr(out), out.stride(0), out.stride(1), out.stride(2), ptr(lse),
-        ptr(ws), ws_bytes, stream_ptr(q.device))
+    with torch.cuda.device(q.device):     # the library launches on the current device
+        rc = L.icsa_sparse_piecewise_attn_fwd(
+            ptr(q), q.stride(0), q.stride(1), q.stride(2),
+            ptr(k), k.stride(0), k.stride(1), k.stride(2),
+            ptr(v), v.stride(0), v.stride(1), v.stride(2),
+            B, H, TQ, TKV, D, float(sparsity),
+            ptr(inj), ptr(idx),
+            ptr(out), out.stride(0), out.stride(1), out.stride(2), ptr(lse),
+            ptr(ws), ws_bytes, stream_ptr(q.device))
     _lib.check("icsa_sparse_piecewise_attn_fwd", rc)
     return out, lse, idx
 
@@ -278,18 +280,19 @@ def sparse_piecewise_attn_1st_intervals_bwd_hip(do, q, k, v, out, lse, indices, 
         raise _lib.IcsaError("icsa_sparse_piecewise_attn_bwd_workspace_size", int(ws_bytes))
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
     g = dtype_code(dq)
-    rc = L.icsa_sparse_piecewise_attn_bwd(
-        ptr(do), do.stride(0), do.stride(1), do.stride(2),
-        ptr(q), q.stride(0), q.stride(1), q.stride(2),
-        ptr(k), k.stride(0), k.stride(1), k.stride(2),
-        ptr(v), v.stride(0), v.stride(1), v.stride(2),
-        ptr(out), out.stride(0), out.stride(1), out.stride(2),
-        ptr(lse), ptr(idx),
-        B, H, TQ, TKV, D, top_k,
-        ptr(dq), g, dq.stride(0), dq.stride(1), dq.stride(2),
-        ptr(dk), g, dk.stride(0), dk.stride(1), dk.stride(2),
-        ptr(dv), g, dv.stride(0), dv.stride(1), dv.stride(2),
-        ptr(ws), ws_bytes, stream_ptr(q.device))
+    with torch.cuda.device(q.device):     # the library launches on the current device
+        rc = L.icsa_sparse_piecewise_attn_bwd(
+            ptr(do), do.stride(0), do.stride(1), do.stride(2),
+            ptr(q), q.stride(0), q.stride(1), q.stride(2),
+            ptr(k), k.stride(0), k.stride(1), k.stride(2),
+            ptr(v), v.stride(0), v.stride(1), v.stride(2),
+            ptr(out), out.stride(0), out.stride(1), out.stride(2),
+            ptr(lse), ptr(idx),
+            B, H, TQ, TKV, D, top_k,
+            ptr(dq), g, dq.stride(0), dq.stride(1), dq.stride(2),
+            ptr(dk), g, dk.stride(0), dk.stride(1), dk.stride(2),
+            ptr(dv), g, dv.stride(0), dv.stride(1), dv.stride(2),
+            ptr(ws), ws_bytes, stream_ptr(q.device))
     _lib.check("icsa_sparse_piecewise_attn_bwd", rc)
     return dq, dk, dv
 
@@ -336,13 +339,14 @@ def flash_attn_func(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, dropout_p
     if ws_bytes < 0:
         raise _lib.IcsaError("icsa_flash_attn_workspace_size", int(ws_bytes))
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
-    rc = L.icsa_flash_attn(
-        ptr(q), q.stride(0), q.stride(1), q.stride(2),
-        ptr(k), k.stride(0), k.stride(1), k.stride(2),
-        ptr(v), v.stride(0), v.stride(1), v.stride(2),
-        B, Sq, Sk, H, D,
-        ptr(out), dtype_code(out), out.stride(0), out.stride(1), out.stride(2),
-        ptr(ws), ws_bytes, stream_ptr(q.device))
+    with torch.cuda.device(q.device):     # the library launches on the current device
+        rc = L.icsa_flash_attn(
+            ptr(q), q.stride(0), q.stride(1), q.stride(2),
+            ptr(k), k.stride(0), k.stride(1), k.stride(2),
+            ptr(v), v.stride(0), v.stride(1), v.stride(2),
+            B, Sq, Sk, H, D,
+            ptr(out), dtype_code(out), out.stride(0), out.stride(1), out.stride(2),
+            ptr(ws), ws_bytes, stream_ptr(q.device))
     _lib.check("icsa_flash_attn", rc)
     return out
 
@@ -367,8 +371,9 @@ def pool(q=None, k=None, v=None, want_vt: bool = False):
             args += [ctypes.c_void_p(0), 0, 0, 0, 0]
         else:
             args += [ptr(t), dtype_code(t), t.stride(0), t.stride(1), t.stride(2)]
-    rc = _lib.lib().icsa_pool(*args, B, S, H, D, ptr(sums[0]), ptr(sums[1]), ptr(sums[2]), ptr(vt),
-                              stream_ptr(ref.device))
+    with torch.cuda.device(ref.device):     # the library launches on the current device
+        rc = _lib.lib().icsa_pool(*args, B, S, H, D, ptr(sums[0]), ptr(sums[1]), ptr(sums[2]), ptr(vt),
+                                  stream_ptr(ref.device))
     _lib.check("icsa_pool", rc)
     return sums[0], sums[1], sums[2], vt
 
@@ -385,9 +390,10 @@ def gather_kv(k: torch.Tensor, v: torch.Tensor, t_seq_len: int, sel: torch.Tenso
     Tp = (Tkv + BLOCK_M - 1) // BLOCK_M * BLOCK_M
     kn = torch.empty(B, H, Tp, D, dtype=torch.bfloat16, device=k.device)
     vn = torch.empty_like(kn)
-    rc = _lib.lib().icsa_gather_kv(
-        ptr(k), dtype_code(k), k.stride(0), k.stride(1), k.stride(2),
-        ptr(v), dtype_code(v), v.stride(0), v.stride(1), v.stride(2),
-        B, S, H, D, t_seq_len, ptr(sel32), topK, ptr(kn), ptr(vn), stream_ptr(k.device))
+    with torch.cuda.device(k.device):     # the library launches on the current device
+        rc = _lib.lib().icsa_gather_kv(
+            ptr(k), dtype_code(k), k.stride(0), k.stride(1), k.stride(2),
+            ptr(v), dtype_code(v), v.stride(0), v.stride(1), v.stride(2),
+            B, S, H, D, t_seq_len, ptr(sel32), topK, ptr(kn), ptr(vn), stream_ptr(k.device))
     _lib.check("icsa_gather_kv", rc)
     return kn, vn

@@ -123,16 +123,17 @@ def wan_qk_prologue(yq: torch.Tensor, yk, norm_q_weight: torch.Tensor, norm_k_we
         a_args = [ptr(a), dtype_code(a), a.stride(0), a.stride(1)]
     ws_bytes = L.icsa_wan_qk_workspace_size(B, S)
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
-    rc = L.icsa_wan_qk_prologue(
-        ptr(yq), ptr(yk), dtype_code(yq), yq.stride(0), yq.stride(1),
-        ptr(wq), ptr(wk), float(eps),
-        ptr(cos), ptr(sin), cos.shape[0],
-        ctypes.cast(_grids(grid_sizes, source_video_grid_sizes, B), ctypes.c_void_p), int(TAG),
-        *a_args,
-        B, S, H, D,
-        ptr(q), ptr(k), q.stride(0), q.stride(1), q.stride(2),
-        ptr(qsum), ptr(ksum), ptr(gate),
-        ptr(ws), ws_bytes, stream_ptr(dev))
+    with torch.cuda.device(dev):     # the library launches on the current device
+        rc = L.icsa_wan_qk_prologue(
+            ptr(yq), ptr(yk), dtype_code(yq), yq.stride(0), yq.stride(1),
+            ptr(wq), ptr(wk), float(eps),
+            ptr(cos), ptr(sin), cos.shape[0],
+            ctypes.cast(_grids(grid_sizes, source_video_grid_sizes, B), ctypes.c_void_p), int(TAG),
+            *a_args,
+            B, S, H, D,
+            ptr(q), ptr(k), q.stride(0), q.stride(1), q.stride(2),
+            ptr(qsum), ptr(ksum), ptr(gate),
+            ptr(ws), ws_bytes, stream_ptr(dev))
     _lib.check("icsa_wan_qk_prologue", rc)
     return q, k, qsum, ksum, gate
 
@@ -199,16 +200,17 @@ def ln_modulate(x: torch.Tensor, shift=None, scale=None, weight=None, bias=None,
     else:
         _require(x_out is None, "x_out needs y")
     o = torch.empty(B, S, dim, dtype=torch.bfloat16, device=x.device) if out else None
-    rc = _lib.lib().icsa_wan_ln_modulate(
-        ptr(x), dtype_code(x), x.stride(0), x.stride(1),
-        ptr(y), y.stride(0) if y is not None else 0, y.stride(1) if y is not None else 0,
-        ptr(gate), gate.stride(0) if gate is not None else 0,
-        ptr(x_out), x_out.stride(0) if x_out is not None else 0,
-        x_out.stride(1) if x_out is not None else 0,
-        ptr(wt), ptr(bs),
-        ptr(shift), ptr(scale), shift.stride(0) if shift is not None else 0, float(eps),
-        B, S, dim, ptr(o), o.stride(0) if o is not None else 0, o.stride(1) if o is not None else 0,
-        stream_ptr(x.device))
+    with torch.cuda.device(x.device):     # the library launches on the current device
+        rc = _lib.lib().icsa_wan_ln_modulate(
+            ptr(x), dtype_code(x), x.stride(0), x.stride(1),
+            ptr(y), y.stride(0) if y is not None else 0, y.stride(1) if y is not None else 0,
+            ptr(gate), gate.stride(0) if gate is not None else 0,
+            ptr(x_out), x_out.stride(0) if x_out is not None else 0,
+            x_out.stride(1) if x_out is not None else 0,
+            ptr(wt), ptr(bs),
+            ptr(shift), ptr(scale), shift.stride(0) if shift is not None else 0, float(eps),
+            B, S, dim, ptr(o), o.stride(0) if o is not None else 0, o.stride(1) if o is not None else 0,
+            stream_ptr(x.device))
     _lib.check("icsa_wan_ln_modulate", rc)
     return o
 

@@ -7,9 +7,10 @@ run in float64 on the GPU as the checker):
 * block sums and the compressed softmax P;
 * every ranked decision -- source blocks, the peaked/diffuse split, the per-block exact
   lists -- must be a valid ranking of the float64 scores within GAP;
-* output rows of seeded-random peaked and diffuse query blocks in every head of every
-  batch entry, against float64 attention for exactly those blocks, built from the GPU's
-  own decisions;
+* output rows of eight seeded-random peaked and eight diffuse query blocks in every head
+  of every batch entry, plus the peaked blocks of the flash grid's last workgroup and the
+  diffuse block whose sparse workgroup starts its sweep furthest along, against float64
+  attention for exactly those blocks, built from the GPU's own decisions;
 * size-independent properties: two runs are bit-identical, and x is exactly linear in
   alpha_2 (x(alpha) - x(0) = alpha * out_c) on every token.
 
@@ -40,7 +41,9 @@ for _flat in (0.25, 0.5, 0.75):
     for _sar, _tag in ((1 / 32, "1/32"), (1 / 16, "1/16"), (1 / 8, "1/8")):
         CASES[f"cfg3-flat{_flat}-sar{_tag}"] = dict(CFG3, flat_ratio=_flat, sar=_sar)
 
-SAMPLES_PER_KIND = 2          # seeded-random peaked and diffuse blocks per (batch, head)
+SAMPLES_PER_KIND = 8          # seeded-random peaked and diffuse blocks per (batch, head)
+SP_SWEEP_CONC = 256           # the sparse kernel's sweep constant (sparse_attn.hip)
+FA_QBLK_PER_WG = 4            # query blocks per flash workgroup (flash_attn.hip)
 
 
 def _block_sums(x, NB):
@@ -49,6 +52,18 @@ def _block_sums(x, NB):
     xp = torch.zeros(B, NB * 64, H, D, dtype=torch.float64, device=x.device)
     xp[:, :S] = x.double()
     return xp.view(B, NB, 64, H, D).sum(2).permute(0, 2, 1, 3)
+
+
+def _max_rotation_slots(B, H, n_diffuse, NKV, device):
+    """Per (batch, head) the diffuse slot whose sparse workgroup starts its exact-list sweep
+    furthest along (the kernel's launch order: work w runs as workgroup 8 (w % per) + w / per,
+    per = ceil(n_work / 8), and starts at new-KV block ((wg / 8) NKV / SP_SWEEP_CONC) % NKV)
+    -> [B, H] positions in the diffuse list."""
+    n_work = B * H * n_diffuse
+    per = -(-n_work // 8)
+    w = torch.arange(n_work, device=device)
+    start = ((w % per) * NKV // SP_SWEEP_CONC) % NKV
+    return start.view(B, H, n_diffuse).argmax(-1, keepdim=True)
 
 
 def _sample(blocks, n, gen):
@@ -125,8 +140,15 @@ def test_full_size_parity(gpu, case):
     # ---- sampled output blocks of every (batch, head), float64 ----
     gs = torch.Generator(device=gpu).manual_seed(1234)
     pk = _sample(peaked, SAMPLES_PER_KIND, gs)                         # [B, H, np]
+    if z.n_peaked > 0:
+        # always the peaked blocks of the flash grid's last workgroup (a partial one when
+        # n_peaked % 4 != 0: its idle slots must leave the real blocks intact)
+        last = list(range(FA_QBLK_PER_WG * ((z.n_peaked - 1) // FA_QBLK_PER_WG), z.n_peaked))
+        pk = torch.cat([pk, peaked[..., last]], -1)
     dpos = _sample(torch.arange(z.n_diffuse, device=gpu).expand(B, H, z.n_diffuse).contiguous(),
                    SAMPLES_PER_KIND, gs)                               # positions in `diffuse`
+    if z.n_diffuse > 0:                                                # and the largest sweep rotation
+        dpos = torch.cat([dpos, _max_rotation_slots(B, H, z.n_diffuse, z.NKV, gpu)], -1)
     dk = torch.gather(diffuse, -1, dpos)                               # [B, H, nd]
     qpad = torch.zeros(B, NB * 64, H, D, dtype=torch.float64, device=gpu)
     qpad[:, :S] = q.double()

@@ -73,3 +73,29 @@ def test_graph_sparse_piecewise(gpu):
     g.replay()
     torch.cuda.synchronize()
     assert torch.equal(out, call()), "replay on new inputs differs from the eager result"
+
+
+def test_graph_editing_noalloc(gpu):
+    # The no-allocation entry point is meant for callers under graph capture: its first call
+    # on a device (the scratch address lookup) happens eagerly in _capture, the captured
+    # call then runs on the static scratch.  Replays must equal eager calls of both entry
+    # points, also after new data is copied into the captured inputs.
+    from icsa_hip.editing_sparse_attention import _editing_sparse_attention_hip
+    print("[case] graph capture icsa_editing_sparse_attention_noalloc H=2 S=4096", flush=True)
+    q0, k0, v0, t = make_inputs(H=2, real=2048, pad=0, kind="random", seed=24)
+    q, k, v = q0.to(gpu), k0.to(gpu), v0.to(gpu)
+
+    def call():
+        return _editing_sparse_attention_hip(q, k, v, t, 0.7, noalloc=True)[0]
+
+    def call_ws():
+        return _editing_sparse_attention_hip(q, k, v, t, 0.7)[0]
+
+    g, out = _capture(call)
+    _check_replays(g, out, call)
+    assert torch.equal(out, call_ws()), "no-alloc replay differs from the workspace entry point"
+    q1, k1, v1, _ = make_inputs(H=2, real=2048, pad=0, kind="random", seed=25)
+    q.copy_(q1.to(gpu)); k.copy_(k1.to(gpu)); v.copy_(v1.to(gpu))
+    g.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(out, call_ws()), "replay on new inputs differs from the workspace entry point"

@@ -133,6 +133,57 @@ def test_sparse_piecewise_interval_bound_skip(gpu):
     compare_out(out, ref)
 
 
+def _pipeline_skip_margins(q, k, t, views):
+    """_interval_skip_margin for the diffuse blocks of one pipeline call (bf16 q, k on the
+    CPU), built from that call's own decisions: the new KV of its source selection and its
+    per-block exact lists."""
+    z = views["sizes"]
+    B, S, H, D = q.shape
+    sel, order, l3 = (views[x].long().cpu() for x in ("sel", "order", "l3"))
+    tokmap = O.new_kv_token_map(t, S, sel)
+    nk = O.gather_new_kv(k, tokmap, torch.float32).to(torch.bfloat16)
+    nk = torch.nn.functional.pad(nk, (0, 0, 0, z["TKV_pad"] - nk.shape[2]))
+    qp = q.permute(0, 2, 1, 3).reshape(B, H, z["NB"], 64, D)
+    diffuse = order[..., z["n_peaked"]:]
+    qd = torch.stack([torch.stack([qp[b, h, diffuse[b, h]] for h in range(H)]) for b in range(B)])
+    return _interval_skip_margin(qd.reshape(B, H, -1, D), nk, l3)
+
+
+def test_interval_skip_is_bit_identical(gpu, monkeypatch):
+    # The interval-bound skip drops interval pass 1 only where it cannot change the running
+    # max, so the output must equal the no-skip schedule bit for bit: the host entry (row-major
+    # V tiles) and an aligned pipeline call (V^T tiles), each with the skip on and off (the
+    # library's ICSA_DEBUG_NO_INTERVAL_SKIP hook).
+    from icsa_hip.editing_sparse_attention import _editing_sparse_attention_hip
+    from icsa_hip.synthetic import make_inputs
+    print("[case] interval skip on / off: host entry", flush=True)
+    TQ, TKV = 256, 64 * 64
+    q, k, v = _bf16(1, 2, TQ, 128, seed=31), _bf16(1, 2, TKV, 128, seed=32), _bf16(1, 2, TKV, 128, seed=33)
+    g = torch.Generator().manual_seed(34)
+    idx = torch.stack([torch.randperm(64, generator=g)[:4].sort().values for _ in range(2 * TQ // 64)])
+    idx = idx.view(1, 2, TQ // 64, 4).to(torch.int32).to(gpu)
+    args = (q.to(gpu), k.to(gpu), v.to(gpu), 0.0625)
+    monkeypatch.delenv("ICSA_DEBUG_NO_INTERVAL_SKIP", raising=False)
+    on = sparse_piecewise_attn_1st_intervals_hip(*args, indices=idx)
+    monkeypatch.setenv("ICSA_DEBUG_NO_INTERVAL_SKIP", "1")
+    off = sparse_piecewise_attn_1st_intervals_hip(*args, indices=idx)
+    monkeypatch.delenv("ICSA_DEBUG_NO_INTERVAL_SKIP")
+    torch.cuda.synchronize()
+    assert torch.equal(on, off)
+
+    print("[case] interval skip on / off: aligned pipeline (V^T tiles)", flush=True)
+    q, k, v, t = make_inputs(H=2, real=2048, pad=0, kind="random", seed=41)
+    qg, kg, vg = q.to(gpu), k.to(gpu), v.to(gpu)
+    on, views = _editing_sparse_attention_hip(qg, kg, vg, t, 0.5, keep_workspace=True)
+    margins = _pipeline_skip_margins(q, k, t, views)
+    assert sum(m > 0.25 for m in margins) >= len(margins) // 2, "the skip must fire in this case"
+    monkeypatch.setenv("ICSA_DEBUG_NO_INTERVAL_SKIP", "1")
+    off, _ = _editing_sparse_attention_hip(qg, kg, vg, t, 0.5)
+    monkeypatch.delenv("ICSA_DEBUG_NO_INTERVAL_SKIP")
+    torch.cuda.synchronize()
+    assert torch.equal(on, off)
+
+
 def test_sparse_piecewise_quirk_case(gpu):
     # Keys of a late chunk align with the queries: the interval's running max rises after
     # earlier chunks were accumulated, which the reference does not rescale.  The oracle

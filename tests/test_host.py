@@ -59,21 +59,34 @@ def test_workspace_layout_is_aligned_and_disjoint():
     n = len(_lib.WS_SLOTS)
     for (S, t, qd) in ((65536, 32768, _lib.BF16), (65520, 32760, _lib.F32), (8192, 4096, _lib.BF16)):
         offs = (ctypes.c_int64 * n)()
-        total = L.icsa_editing_workspace_layout(1, S, 40, 128, t, 0.0625, 0.125, 0.5, qd, qd,
+        total = L.icsa_editing_workspace_layout(1, S, 40, 128, t, 0.0625, 0.125, 0.5, qd, qd, qd,
                                                 ctypes.cast(offs, ctypes.c_void_p))
         assert total > 0
-        assert total == L.icsa_editing_workspace_size(1, S, 40, 128, t, 0.0625, 0.125, 0.5, qd, qd)
+        assert total == L.icsa_editing_workspace_size(1, S, 40, 128, t, 0.0625, 0.125, 0.5, qd, qd, qd)
         o = list(offs)
         assert all(x % 256 == 0 and 0 <= x <= total for x in o)
         assert o == sorted(o)
     # block sums of the new v: transposed for the V^T tiles of aligned t, row-major for the
-    # row tiles of the materialised new KV (t % 64 != 0); no transposed copy of the new V
-    vc, vct = _lib.WS_SLOTS.index("VC"), _lib.WS_SLOTS.index("VCT")
-    for t, want_vc in ((32768, False), (32760, True)):
+    # row tiles the sparse kernel reads in place when t % 64 != 0; a bf16 copy of v only for
+    # an f32 v at unaligned t
+    vc, vct, vb = (_lib.WS_SLOTS.index(x) for x in ("VC", "VCT", "VB"))
+    for t, vd, want_vc, want_vb in ((32768, _lib.BF16, False, False), (32760, _lib.BF16, True, False),
+                                    (32768, _lib.F32, False, False), (32760, _lib.F32, True, True)):
         offs = (ctypes.c_int64 * n)()
         L.icsa_editing_workspace_layout(1, 65536, 40, 128, t, 0.0625, 0.125, 0.5, _lib.BF16, _lib.BF16,
-                                        ctypes.cast(offs, ctypes.c_void_p))
+                                        vd, ctypes.cast(offs, ctypes.c_void_p))
         assert (offs[vc + 1] > offs[vc]) == want_vc and (offs[vct + 1] > offs[vct]) != want_vc
+        assert (offs[vb + 1] > offs[vb]) == want_vb
+
+
+def test_unaligned_workspace_holds_no_materialised_new_kv():
+    # t % 64 != 0 reads the straddling new-KV blocks in place: the workspace of configuration
+    # 4's shape is the aligned one's plus the row-major new-KV value sums, nothing of size Tkv
+    L = _lib.lib()
+    args = (1, 65520, 40, 128)
+    aligned = L.icsa_editing_workspace_size(*args, 32768, 0.0625, 0.125, 0.5, _lib.BF16, _lib.BF16, _lib.BF16)
+    unaligned = L.icsa_editing_workspace_size(*args, 32760, 0.0625, 0.125, 0.5, _lib.BF16, _lib.BF16, _lib.BF16)
+    assert 0 < unaligned < aligned + 8 * 2**20, (aligned, unaligned)
 
 
 def _status(name, *args):

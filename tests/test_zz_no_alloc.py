@@ -32,7 +32,8 @@ def test_noalloc_matches_workspace_entry_point(gpu):
         B, S, H, D = q.shape
         need = _lib.lib().icsa_editing_workspace_size(B, S, H, D, t, c["sar"], 0.125, c["flat"],
                                                       0 if q.dtype == torch.bfloat16 else 1,
-                                                      0 if k.dtype == torch.bfloat16 else 1)
+                                                      0 if k.dtype == torch.bfloat16 else 1,
+                                                      0 if v.dtype == torch.bfloat16 else 1)
         print(f"[noalloc] call {i}: B={B} S={S} H={H} t={t} workspace {need / 2**20:.1f} MiB "
               f"of {_lib.NOALLOC_SCRATCH_BYTES / 2**20:.0f} MiB", flush=True)
         assert 0 < need <= _lib.NOALLOC_SCRATCH_BYTES
