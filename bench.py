@@ -48,17 +48,22 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def load_traffic(path):
-    """HBM bytes per launch of the dominant kernel from a committed rocprofv3 summary
-    (line ``traffic_bytes_per_launch: N``), or None."""
+def load_profile(path):
+    """Figures of the dominant kernel from a committed rocprofv3 summary: its lines
+    ``traffic_bytes_per_launch: N`` (HBM bytes per launch from the FETCH_SIZE / WRITE_SIZE
+    passes), ``kernel_avg_us: T`` (the traced average duration) and ``profile_date: D``.
+    Missing entries are None."""
+    keys = {"traffic_bytes_per_launch": float, "kernel_avg_us": float, "profile_date": str}
+    out = dict.fromkeys(keys)
     try:
         with open(path) as f:
             for line in f:
-                if line.strip().startswith("traffic_bytes_per_launch:"):
-                    return float(line.split(":", 1)[1])
+                name, _, val = line.strip().partition(":")
+                if name in keys and val.strip():
+                    out[name] = keys[name](val.strip())
     except OSError:
-        return None
-    return None
+        pass
+    return out
 
 
 CPU_SHARE = 16
@@ -562,21 +567,25 @@ def main():
     pool_moved = pool_bytes + BH * D * (-(-t // 64) * 64) * 2
     comp_bytes = 3 * BH * NB * D * 4 + BH * NB * NB * 4 + BH * NB * D * 4
 
-    # KV gather (materialised new KV of the drop-in path) on this call's selection
-    out, views = _editing_sparse_attention_hip(q, k, v, t, 1.0, args.sar, 0.125, args.flat_ratio,
-                                               keep_workspace=True)
-    sel = views["sel"].clone()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    gather_kv(k, v, t, sel)
-    e0.record(stream)
-    for _ in range(5):
+    # The layer reads the new KV in place (the attention kernels gather its blocks by index);
+    # the standalone gather entry point (icsa_gather_kv: the materialised new KV that the
+    # reference builds) is timed on this call's selection at the headline configuration only
+    gather_ms = gather_bytes = None
+    if args.config == 2:
+        out, views = _editing_sparse_attention_hip(q, k, v, t, 1.0, args.sar, 0.125, args.flat_ratio,
+                                                   keep_workspace=True)
+        sel = views["sel"].clone()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         gather_kv(k, v, t, sel)
-    e1.record(stream)
-    torch.cuda.synchronize()
-    gather_ms = e0.elapsed_time(e1) / 5
-    Tp = z["TKV_pad"]
-    gather_bytes = 2 * (BH * z["Tkv"] * D * 2) + 2 * (BH * Tp * D * 2)
-    del out, views
+        e0.record(stream)
+        for _ in range(5):
+            gather_kv(k, v, t, sel)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        gather_ms = e0.elapsed_time(e1) / 5
+        Tp = z["TKV_pad"]
+        gather_bytes = 2 * (BH * z["Tkv"] * D * 2) + 2 * (BH * Tp * D * 2)
+        del out, views
 
     dense = None
     if not args.no_dense:
@@ -607,7 +616,8 @@ def main():
 
     fa_ms = stage_ms["flash"]
     fa_tflops = fa_flops / fa_ms / 1e9
-    traffic = load_traffic(os.path.join(ROOT, "profiles", "flash_attn_peaked_cfg2.md"))
+    prof_path = os.path.join("profiles", "flash_attn_peaked_cfg2.md")
+    prof = load_profile(os.path.join(ROOT, prof_path))
     result = {
         "metric": "sparse-attn layer ms + TFLOP/s at 65K tok H=40 D=128; speedup vs dense FA",
         "value": dense_flops / ms_per_step / 1e9,
@@ -634,15 +644,26 @@ def main():
             "pool": pool_bytes / stage_ms["pool"] / 1e6,
             "pool_moved": pool_moved / stage_ms["pool"] / 1e6,
             "compressed": comp_bytes / stage_ms["compressed"] / 1e6,
-            "kv_gather": gather_bytes / gather_ms / 1e6,
+            "kv_gather": gather_bytes / gather_ms / 1e6 if gather_ms else None,
         },
         "mfma_frac": {"flash": fa_tflops / PEAK_BF16_TFLOPS,
                       "sparse": sparse_flops / stage_ms["sparse"] / 1e9 / PEAK_BF16_TFLOPS},
         "roofline": {"bound": "mfma", "achieved": fa_tflops, "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": fa_tflops / PEAK_BF16_TFLOPS,
-                     "traffic": traffic,
+                     "traffic": prof["traffic_bytes_per_launch"],
                      "kernel": "icsa_flash_kernel (peaked query blocks)",
-                     "flops_per_launch": fa_flops},
+                     "flops_per_launch": fa_flops,
+                     # traffic is not measurable in this run (it needs two rocprofv3 --pmc
+                     # passes); the profile it comes from, its traced kernel average and the
+                     # fraction at that average, so this line and profiles/ can be checked
+                     # against each other
+                     "profile": {"path": prof_path, "date": prof["profile_date"],
+                                 "kernel_avg_us": prof["kernel_avg_us"],
+                                 "frac_at_kernel_avg": (fa_flops / (prof["kernel_avg_us"] * 1e6)
+                                                        / PEAK_BF16_TFLOPS
+                                                        if prof["kernel_avg_us"] else None),
+                                 "event_vs_trace": (fa_ms * 1e3 / prof["kernel_avg_us"]
+                                                    if prof["kernel_avg_us"] else None)}},
     }
     if not args.no_wan:
         del q, k, v
