@@ -203,6 +203,20 @@ int icsa_sparse_piecewise_attn(
     void* out, int64_t o_sb, int64_t o_sh, int64_t o_st,
     void* workspace, int64_t workspace_bytes, void* stream);
 
+/* sparse_piecewise_attn_tilelang_hosttopk (tilelang_host.py:121-226): the same function as
+ * icsa_sparse_piecewise_attn with the interval taken over chunks of interval_bn (= BN: 16,
+ * 32 or 64) compressed blocks, which decides where the non-rescaled interval terms take
+ * their running max (tilelang_kernels.py:886-978).  interval_bn = 64 equals
+ * icsa_sparse_piecewise_attn.  Workspace: icsa_sparse_piecewise_workspace_size. */
+int icsa_sparse_piecewise_attn_hosttopk(
+    const void* q, int64_t q_sb, int64_t q_sh, int64_t q_st,
+    const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st,
+    const void* v, int64_t v_sb, int64_t v_sh, int64_t v_st,
+    int B, int H, int TQ, int TKV, int D, double sparsity, int interval_bn,
+    const int32_t* inject_idx, int32_t* idx_out,
+    void* out, int64_t o_sb, int64_t o_sh, int64_t o_st,
+    void* workspace, int64_t workspace_bytes, void* stream);
+
 /* The Triton host's forward (workspace: icsa_sparse_piecewise_workspace_size) with the state
  * its backward needs.  Contract of triton_host.py:11-30 / triton_kernels.py:489-539: TQ and
  * TKV need not be multiples of 64 (rows past them read as zeros in the block sums); the

@@ -377,6 +377,7 @@ int editing_impl(ICSA_EDITING_ARGS, void* const* stage_events, const float* qsum
     s.qblocks = order; s.qb_offset = z.n_peaked; s.qb_stride = z.NB; s.n_qblk = z.n_diffuse;
     s.kvmap = sp.kvmap; s.kvmap_identity = 0;
     s.seg_a = seg_a; s.seg_from = z.n_t;
+    s.interval_bn = ICSA_BLOCK;        // the TileLang pipeline's BN (tilelang_host.py:127)
     s.idx = l3; s.top_k = z.top_k; s.NKV = z.NKV; s.NKVp = z.NKVp;
     s.kc = np.kc; s.vct = np.vct; s.vc = np.vc;
     s.out_c = cp.out_c; s.nb_q = z.NB;
@@ -660,9 +661,11 @@ static int sparse_piecewise_impl(
     int B, int H, int TQ, int TKV, int D, double sparsity,
     const int32_t* inject_idx, int32_t* idx_out,
     void* out, int64_t o_sb, int64_t o_sh, int64_t o_st, float* lse_out,
-    void* workspace, int64_t workspace_bytes, void* stream_, int triton) {
+    void* workspace, int64_t workspace_bytes, void* stream_, int triton, int interval_bn) {
   int rc = validate_common(B, TQ, H, D);
   if (rc) return rc;
+  if (interval_bn != 16 && interval_bn != 32 && interval_bn != 64)
+    return fail(ICSA_EUNSUPPORTED, "interval chunk BN=%d unsupported (16, 32 or 64)", interval_bn);
   if (TKV <= 0) return fail(ICSA_EINVAL, "TKV must be positive");
   if (!triton && (TQ % ICSA_BLOCK || TKV % ICSA_BLOCK))
     return fail(ICSA_EINVAL, "TQ/TKV must be divisible by the block size 64 (got %d, %d)", TQ, TKV);
@@ -742,6 +745,7 @@ static int sparse_piecewise_impl(
   s.scale_log2 = kLog2e / std::sqrt((float)ICSA_D);
   s.lse = lse_out;
   s.mask_tail = triton;
+  s.interval_bn = interval_bn;
   // the block top-k score rows are free again: BH * min(8, cdiv(NKV, 16)) floats of them hold the
   // |KC_j| bound of the interval pass
   if (interval_skip_enabled()) {
@@ -763,7 +767,20 @@ int icsa_sparse_piecewise_attn(
     void* workspace, int64_t workspace_bytes, void* stream) {
   return sparse_piecewise_impl(q, q_sb, q_sh, q_st, k, k_sb, k_sh, k_st, v, v_sb, v_sh, v_st, B, H,
                                TQ, TKV, D, sparsity, inject_idx, idx_out, out, o_sb, o_sh, o_st,
-                               nullptr, workspace, workspace_bytes, stream, 0);
+                               nullptr, workspace, workspace_bytes, stream, 0, ICSA_BLOCK);
+}
+
+int icsa_sparse_piecewise_attn_hosttopk(
+    const void* q, int64_t q_sb, int64_t q_sh, int64_t q_st,
+    const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st,
+    const void* v, int64_t v_sb, int64_t v_sh, int64_t v_st,
+    int B, int H, int TQ, int TKV, int D, double sparsity, int interval_bn,
+    const int32_t* inject_idx, int32_t* idx_out,
+    void* out, int64_t o_sb, int64_t o_sh, int64_t o_st,
+    void* workspace, int64_t workspace_bytes, void* stream) {
+  return sparse_piecewise_impl(q, q_sb, q_sh, q_st, k, k_sb, k_sh, k_st, v, v_sb, v_sh, v_st, B, H,
+                               TQ, TKV, D, sparsity, inject_idx, idx_out, out, o_sb, o_sh, o_st,
+                               nullptr, workspace, workspace_bytes, stream, 0, interval_bn);
 }
 
 int icsa_sparse_piecewise_attn_fwd(
@@ -777,7 +794,7 @@ int icsa_sparse_piecewise_attn_fwd(
   if (!idx_out || !lse_out) return fail(ICSA_EINVAL, "idx_out and lse_out are required (saved for the backward)");
   return sparse_piecewise_impl(q, q_sb, q_sh, q_st, k, k_sb, k_sh, k_st, v, v_sb, v_sh, v_st, B, H,
                                TQ, TKV, D, sparsity, inject_idx, idx_out, out, o_sb, o_sh, o_st,
-                               lse_out, workspace, workspace_bytes, stream, 1);
+                               lse_out, workspace, workspace_bytes, stream, 1, ICSA_BLOCK);
 }
 
 // ---------------------------------------------------------------------------------------

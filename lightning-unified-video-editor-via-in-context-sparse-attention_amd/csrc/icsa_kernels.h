@@ -178,6 +178,9 @@ struct SparseParams {
   // optional [BH, kc_bound_n] partial maxima of |KC_j| (launch_kc_bound): a workgroup whose
   // rows all satisfy |q| max |KC_j| c / 64 < exact max skips the interval max pass
   const float* kc_bound; int kc_bound_n;
+  // blocks per interval chunk of the reference (BN): the running max of the non-rescaled
+  // interval terms is taken per chunk of that many blocks; 64, or 16 / 32 (row-major V)
+  int interval_bn;
 };
 hipError_t launch_sparse(const SparseParams& p, hipStream_t stream);
 // out[bh * G + y] = max over the new-KV blocks j < NKV with (j / 16) % G == y of the L2

@@ -510,16 +510,45 @@ icsa_sparse_kernel(SparseParams p) {
     ATT_BARRIER();
     const bool more = g + 1 < T;
     if (more) issue_k(g + 1);
-    m_c = fmaxf(m_c, interval_z(ch));
     float rs = 0.f;
+    if (!VROW || SEG || p.interval_bn == ATT_BN) {
+      m_c = fmaxf(m_c, interval_z(ch));
 #pragma unroll
-    for (int sub = 0; sub < 2; ++sub)
+      for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const float e = __builtin_amdgcn_exp2f(fmaf(s[sub][i], c64, -m_c));
-        rs += e;
-        pf[2 * sub + (i >> 3)][i & 7] = (bf16)e;
+        for (int i = 0; i < 16; ++i) {
+          const float e = __builtin_amdgcn_exp2f(fmaf(s[sub][i], c64, -m_c));
+          rs += e;
+          pf[2 * sub + (i >> 3)][i & 7] = (bf16)e;
+        }
+    } else {
+      // reference chunks of BN = 16 or 32 blocks (tilelang_kernels.py:886-978 with a
+      // smaller BN): the running max takes each sub-chunk's max in turn, in block order.
+      // Quarter u (16 blocks) of the tile: sub-tile u / 2, accumulator elements
+      // 8 (u % 2) .. + 7 (blocks 8 (i / 4) + 4 hl + i % 4 of the sub-tile).
+      interval_z(ch);                    // masks selected blocks and blocks >= NKV
+      const int per = p.interval_bn >> 4;  // quarters per reference chunk: 1 or 2
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        if ((u & (per - 1)) == 0) {
+          float mx = -INFINITY;
+#pragma unroll
+          for (int x = 0; x < 2; ++x)
+            if (x < per) {
+              const int uu = u + x;
+#pragma unroll
+              for (int i = 0; i < 8; ++i) mx = fmaxf(mx, s[uu >> 1][8 * (uu & 1) + i]);
+            }
+          m_c = fmaxf(m_c, xhalf_max(mx) * c64);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float e = __builtin_amdgcn_exp2f(fmaf(s[u >> 1][8 * (u & 1) + i], c64, -m_c));
+          rs += e;
+          pf[u][i] = (bf16)e;
+        }
       }
+    }
     gl_run += rs;
     if (more) SP_WAIT_OLDER();             // V(g); K(g + 1) is the newer tile in flight
     else SP_WAIT_ALL();
@@ -592,6 +621,9 @@ hipError_t launch_sparse(const SparseParams& p, hipStream_t stream) {
     return hipErrorInvalidValue;
   if (p.v_rows ? ((int64_t)p.Sk * p.v_st * 2 > 0x7fffffffLL || 64LL * p.v_st * 2 > 0x7fffffffLL || !p.vc)
                : ((int64_t)ICSA_D * p.vt_sd * 2 > 0x7fffffffLL || !p.vct))
+    return hipErrorInvalidValue;
+  // reference interval chunks of 16 or 32 blocks: the host entry points (row-major V)
+  if (!(p.interval_bn == ATT_BN || ((p.interval_bn == 16 || p.interval_bn == 32) && p.v_rows && p.seg_a == 0)))
     return hipErrorInvalidValue;
   // straddling blocks: row-major V, seg_a in [0, 64), no Triton-style tail mask
   if (p.seg_a < 0 || p.seg_a >= ATT_BN || (p.seg_a > 0 && (!p.v_rows || p.mask_tail || p.seg_from < 0)))

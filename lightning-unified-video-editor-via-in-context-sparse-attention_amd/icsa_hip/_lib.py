@@ -45,7 +45,7 @@ EXPORTS = [
     "icsa_pool", "icsa_gather_kv", "icsa_wan_qk_workspace_size", "icsa_wan_qk_prologue",
     "icsa_editing_sparse_attention_presummed", "icsa_wan_ln_modulate", "icsa_last_error",
     "icsa_version", "icsa_sparse_piecewise_attn_fwd", "icsa_sparse_piecewise_attn_bwd_workspace_size",
-    "icsa_sparse_piecewise_attn_bwd",
+    "icsa_sparse_piecewise_attn_bwd", "icsa_sparse_piecewise_attn_hosttopk",
 ]
 
 _p = ctypes.c_void_p
@@ -91,6 +91,14 @@ _SIGNATURES = {
         _p, _l, _l, _l,
         _p, _l, _l, _l,
         _i, _i, _i, _i, _i, _d,
+        _p, _p,
+        _p, _l, _l, _l,
+        _p, _l, _p]),
+    "icsa_sparse_piecewise_attn_hosttopk": (_i, [
+        _p, _l, _l, _l,
+        _p, _l, _l, _l,
+        _p, _l, _l, _l,
+        _i, _i, _i, _i, _i, _d, _i,
         _p, _p,
         _p, _l, _l, _l,
         _p, _l, _p]),

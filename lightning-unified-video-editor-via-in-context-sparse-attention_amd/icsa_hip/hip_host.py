@@ -79,7 +79,7 @@ def ptr(t):
 def sparse_piecewise_attn_1st_intervals_hip(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                                             sparsity: float = 0.1, block_size: int = 64, *,
                                             indices: torch.Tensor = None,
-                                            return_indices: bool = False):
+                                            return_indices: bool = False, interval_bn: int = 64):
     """Sparse piecewise attention (first-order intervals) on MI355X.
 
     Args:
@@ -91,6 +91,7 @@ def sparse_piecewise_attn_1st_intervals_hip(q: torch.Tensor, k: torch.Tensor, v:
         indices: optional [B, H, TQ/64, top_k] int32 block lists (ascending) to use instead
             of the kernel's own top-k (testing hook; not in the reference signature)
         return_indices: also return the block lists used
+        interval_bn: blocks per interval chunk (the TileLang kernel's BN: 16, 32 or 64)
 
     Returns:
         out: [B, H, TQ, D] bfloat16 (a new tensor owned by the caller)
@@ -122,16 +123,21 @@ def sparse_piecewise_attn_1st_intervals_hip(q: torch.Tensor, k: torch.Tensor, v:
         _require(tuple(inj.shape) == (B, H, NQ, top_k), f"indices must be [B, H, {NQ}, {top_k}]")
         check_index_lists(inj, NKV, "indices")
     idx_out = torch.empty(B, H, NQ, top_k, dtype=torch.int32, device=q.device) if return_indices else None
+    args = ([ptr(q), q.stride(0), q.stride(1), q.stride(2),
+             ptr(k), k.stride(0), k.stride(1), k.stride(2),
+             ptr(v), v.stride(0), v.stride(1), v.stride(2),
+             B, H, TQ, TKV, D, float(sparsity)],
+            [ptr(inj), ptr(idx_out),
+             ptr(out), out.stride(0), out.stride(1), out.stride(2),
+             ptr(ws), ws_bytes, stream_ptr(q.device)])
     with torch.cuda.device(q.device):     # the library launches on the current device
-        rc = L.icsa_sparse_piecewise_attn(
-            ptr(q), q.stride(0), q.stride(1), q.stride(2),
-            ptr(k), k.stride(0), k.stride(1), k.stride(2),
-            ptr(v), v.stride(0), v.stride(1), v.stride(2),
-            B, H, TQ, TKV, D, float(sparsity),
-            ptr(inj), ptr(idx_out),
-            ptr(out), out.stride(0), out.stride(1), out.stride(2),
-            ptr(ws), ws_bytes, stream_ptr(q.device))
-    _lib.check("icsa_sparse_piecewise_attn", rc)
+        if interval_bn == BLOCK_M:
+            name = "icsa_sparse_piecewise_attn"
+            rc = L.icsa_sparse_piecewise_attn(*args[0], *args[1])
+        else:
+            name = "icsa_sparse_piecewise_attn_hosttopk"
+            rc = L.icsa_sparse_piecewise_attn_hosttopk(*args[0], int(interval_bn), *args[1])
+    _lib.check(name, rc)
     return (out, idx_out) if return_indices else out
 
 
@@ -145,19 +151,18 @@ def sparse_piecewise_attn_tilelang_hosttopk_hip(q, k, v, sparsity=0.0625, BT=64,
     interval over the rest.  The reference's two paths (the fused kernel when ``BV == Vdim``,
     the top-k + interval kernel pair otherwise) compute the same function; here one kernel
     serves both, so ``BV`` only has to divide Vdim.  ``BN`` is the interval chunk size,
-    which decides where the non-rescaled interval terms take their running max: 64 is the
-    one this kernel implements (the reference's default and the value every reference
-    caller passes).  ``threads_*``, ``sorted_topk`` (the exact loop's visiting order only
-    changes rounding) and ``fused_use_wgmma`` select reference launch variants and have
-    no effect here."""
+    which decides where the non-rescaled interval terms take their running max: 16, 32
+    and 64 (the reference's default, which every reference caller passes) run here.
+    ``threads_*``, ``sorted_topk`` (the exact loop's visiting order only changes rounding)
+    and ``fused_use_wgmma`` select reference launch variants and have no effect here."""
     assert q.dtype == k.dtype == v.dtype == torch.bfloat16
     _require(q.ndim == 4 and k.ndim == 4 and v.ndim == 4, "q, k, v must be 4-D [B, H, T, D]")
     TQ, TKV, Vdim = q.shape[2], k.shape[2], v.shape[3]
     assert TQ % BT == 0 and TKV % BT == 0, "TQ/TKV must be divisible by BT"
     assert Vdim % BV == 0, "Vdim must be divisible by BV"
     _require(BT == BLOCK_M, f"BT={BT} unsupported (the kernels use 64-row blocks)")
-    _require(BN == 64, f"BN={BN} unsupported (the interval runs over chunks of 64 blocks)")
-    return sparse_piecewise_attn_1st_intervals_hip(q, k, v, sparsity, BT)
+    _require(BN in (16, 32, 64), f"BN={BN} unsupported (16, 32 or 64 blocks per interval chunk)")
+    return sparse_piecewise_attn_1st_intervals_hip(q, k, v, sparsity, BT, interval_bn=BN)
 
 
 def _check_sparse_args(q, k, v, block_size, aligned=True):

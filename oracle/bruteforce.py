@@ -54,11 +54,12 @@ def bf_compressed(qc, kc, vc):
     return P, out
 
 
-def bf_sparse_piecewise(q, k, v, sparsity, order_exact=None, triton=False):
+def bf_sparse_piecewise(q, k, v, sparsity, order_exact=None, triton=False, bn=64):
     """One (b,h) of the sparse kernel, scalar loops.  q [TQ,D], k/v [TKV,D].
 
     For every query row: online softmax over the selected blocks key by key, then the
-    interval chunks (64 compressed blocks each) with the non-rescaled g_acc/g_l.
+    interval chunks (``bn`` compressed blocks each, 64 by default) with the non-rescaled
+    g_acc/g_l.
     ``order_exact`` optionally fixes the per-block index lists (any order).
     ``triton``: the Triton host's contract (triton_kernels.py:489-539): TQ and TKV need not
     be multiples of 64; a block's sums run over its real rows, the exact loop visits only
@@ -95,8 +96,8 @@ def bf_sparse_piecewise(q, k, v, sparsity, order_exact=None, triton=False):
                     acc = acc * a + p * v[key]
                     m = m_new
             g_acc, g_l = np.zeros(D), 0.0
-            for c0 in range(0, NKV, 64):
-                chunk = range(c0, min(NKV, c0 + 64))
+            for c0 in range(0, NKV, bn):
+                chunk = range(c0, min(NKV, c0 + bn))
                 svals = {}
                 for j in chunk:
                     if j in sel:

@@ -287,7 +287,7 @@ def dense_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
 def sparse_piecewise_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                           sparsity: float = 0.1, indices: Optional[torch.Tensor] = None,
                           dtype=torch.float64, qchunk: int = 64, return_lse: bool = False,
-                          mode: str = "tilelang"):
+                          mode: str = "tilelang", bn: int = BN_INTERVAL):
     """Sparse piecewise attention with the first-order interval approximation.
 
     ``mode="triton"`` follows the Triton host instead (triton_host.py:11-30 ->
@@ -308,7 +308,8 @@ def sparse_piecewise_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
       (tilelang_host.py:171-173).  Default: ranked order; the exact loop visits them in
       ascending block index (the loop order only changes rounding).
     * Exact online softmax over those blocks (tilelang_kernels.py:863-868).
-    * Interval over chunks of 64 compressed blocks in ascending order
+    * Interval over chunks of ``bn`` compressed blocks (the TileLang kernel's BN, 64 by
+      default, tilelang_host.py:127) in ascending order
       (tilelang_kernels.py:886-978): score ``q . KC_j / 64`` (-inf for selected blocks and
       blocks >= NKV); the running max and ``acc``/``l`` are rescaled, but ``g_acc`` and
       ``g_l`` (``+= p VC``, ``+= 64 sum p``) are *not* rescaled when the max grows later.
@@ -341,7 +342,7 @@ def sparse_piecewise_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         indices = ranked_topk(scores, top_k)
     indices = torch.sort(indices.long().to(dev), dim=-1).values
     assert indices.shape == (B, H, NQ, top_k)
-    n_chunks = ceil_div(NKV, BN_INTERVAL)
+    n_chunks = ceil_div(NKV, bn)
     kb = kd.view(B, H, NKV, BLOCK_M, D)
     vb = vd.view(B, H, NKV, BLOCK_M, D)
     out = torch.empty(B, H, TQ, D, dtype=dtype, device=dev)
@@ -370,7 +371,7 @@ def sparse_piecewise_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         g_acc = torch.zeros_like(acc)
         g_l = torch.zeros_like(l)
         for c in range(n_chunks):
-            j0, j1 = c * BN_INTERVAL, min(NKV, (c + 1) * BN_INTERVAL)
+            j0, j1 = c * bn, min(NKV, (c + 1) * bn)
             s_c = s_int[..., j0:j1]
             m_new = torch.maximum(m, s_c.max(-1).values)
             alpha = torch.exp(m - m_new)

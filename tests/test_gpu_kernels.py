@@ -91,8 +91,12 @@ def test_tilelang_hosttopk_entry(gpu):
         got = sparse_piecewise_attn_tilelang_hosttopk_hip(q, k, v, 0.0625, BT=64, BV=bv, BN=64,
                                                           sorted_topk=srt)
         assert torch.equal(got, want)
+    # BN = 16 / 32 run (their results: test_hosttopk_interval_chunk_size); others are refused
+    for bn in (16, 32):
+        got = sparse_piecewise_attn_tilelang_hosttopk_hip(q, k, v, 0.0625, BN=bn)
+        assert torch.isfinite(got.float()).all()
     with pytest.raises(IcsaArgumentError):
-        sparse_piecewise_attn_tilelang_hosttopk_hip(q, k, v, BN=32)
+        sparse_piecewise_attn_tilelang_hosttopk_hip(q, k, v, BN=48)
 
 
 def _interval_skip_margin(q, k, idx):
@@ -182,6 +186,45 @@ def test_interval_skip_is_bit_identical(gpu, monkeypatch):
     monkeypatch.delenv("ICSA_DEBUG_NO_INTERVAL_SKIP")
     torch.cuda.synchronize()
     assert torch.equal(on, off)
+
+
+@pytest.mark.parametrize("bn", [16, 32, 64])
+def test_hosttopk_interval_chunk_size(gpu, bn):
+    # BN (sparse_piecewise_attn_tilelang_hosttopk's interval chunk) decides where the
+    # non-rescaled interval terms take their running max.  (i) Two interval peaks, blocks 20
+    # (logit 2) and 40 (logit 4): one chunk for BN = 64 (plain softmax over the peaks), two
+    # for BN = 32 and 16 (the first peak keeps the smaller max) -- the results differ by
+    # more than 0.3, and each matches the oracle with that BN.  (ii) Random keys with the
+    # exact lists injected as the lowest-scoring blocks, so the running max rises chunk by
+    # chunk, against the oracle with that BN.
+    print(f"[case] hosttopk BN={bn}", flush=True)
+    D, NKV = 128, 128
+    q = torch.zeros(1, 1, 64, D)
+    q[..., 0] = 1.0
+    k = torch.zeros(1, 1, NKV * 64, D)
+    k[..., 0] = -1000.0 * math.sqrt(D)
+    v = torch.zeros(1, 1, NKV * 64, D)
+    for blk, logit, d in ((0, 0.0, 0), (20, 2.0, 1), (40, 4.0, 2)):
+        k[0, 0, 64 * blk:64 * (blk + 1), 0] = logit * math.sqrt(D)
+        v[0, 0, 64 * blk:64 * (blk + 1), d] = 1.0        # output dim d = the block's weight
+    q, k, v = q.to(torch.bfloat16), k.to(torch.bfloat16), v.to(torch.bfloat16)
+    idx = torch.zeros(1, 1, 1, 1, dtype=torch.int32)
+    outs = {}
+    for b in sorted({bn, 64}):
+        outs[b] = sparse_piecewise_attn_1st_intervals_hip(q.to(gpu), k.to(gpu), v.to(gpu), 0.008,
+                                                          indices=idx.to(gpu), interval_bn=b)
+    ref, _, _ = O.sparse_piecewise_attn(q, k, v, 0.008, indices=idx.long(), bn=bn)
+    compare_out(outs[bn], ref)
+    if bn != 64:
+        assert (outs[bn].float() - outs[64].float()).abs().max().item() > 0.3
+    q2, k2, v2 = _bf16(1, 2, 256, D, seed=41), _bf16(1, 2, 130 * 64, D, seed=42), _bf16(1, 2, 130 * 64, D, seed=43)
+    qc = q2.double().view(1, 2, 4, 64, D).sum(3)
+    kc = k2.double().view(1, 2, 130, 64, D).sum(3)
+    low = torch.matmul(qc, kc.transpose(-1, -2)).argsort(-1)[..., :6].sort(-1).values.to(torch.int32)
+    out2 = sparse_piecewise_attn_1st_intervals_hip(q2.to(gpu), k2.to(gpu), v2.to(gpu), 0.05,
+                                                   indices=low.to(gpu), interval_bn=bn)
+    ref2, _, _ = O.sparse_piecewise_attn(q2, k2, v2, 0.05, indices=low.long(), bn=bn)
+    compare_out(out2, ref2)
 
 
 def test_sparse_piecewise_quirk_case(gpu):

@@ -255,6 +255,66 @@ def test_sparse_interval_accumulators_are_not_rescaled():
     assert np.allclose(ob, quirk.expand(64, 4).numpy(), atol=1e-15)
 
 
+def _two_peak_case(b1, b2):
+    """One query block against 128 key blocks: exact block 0 logit 0, block b1 logit 2,
+    block b2 logit 4, every other block -1000; value of block 0 / b1 / b2 = e0 / e1 / e2."""
+    D = 4
+    q = torch.zeros(1, 1, 64, D, dtype=DT)
+    q[..., 0] = 1.0
+    k = torch.zeros(1, 1, 128 * 64, D, dtype=DT)
+    k[..., 0] = -1000.0 * math.sqrt(D)
+    v = torch.zeros(1, 1, 128 * 64, D, dtype=DT)
+    for blk, logit, d in ((0, 0.0, 0), (b1, 2.0, 1), (b2, 4.0, 2)):
+        k[0, 0, 64 * blk:64 * (blk + 1), 0] = logit * math.sqrt(D)
+        v[0, 0, 64 * blk:64 * (blk + 1), d] = 1.0
+    return q, k, v, torch.zeros(1, 1, 1, 1, dtype=torch.long)
+
+
+@pytest.mark.parametrize("b1,b2,bn,same_chunk", [(5, 40, 64, True), (5, 40, 32, False), (5, 40, 16, False),
+                                                 (5, 20, 32, True), (5, 20, 16, False)])
+def test_sparse_interval_chunk_size_sets_the_running_max(b1, b2, bn, same_chunk):
+    # BN (blocks per interval chunk, tilelang_host.py:127) decides where the non-rescaled
+    # interval terms take their running max.  Two interval peaks in one chunk share the
+    # chunk's max -- the terms are consistent and the result is plain softmax over the
+    # three blocks; in different chunks the first peak's terms keep the older, smaller max
+    # (the reference's non-rescaled g_acc / g_l).  Closed forms, oracle and brute force.
+    q, k, v, idx = _two_peak_case(b1, b2)
+    out, _, _ = O.sparse_piecewise_attn(q, k, v, sparsity=0.008, indices=idx, bn=bn)
+    e4, e2 = math.exp(-4.0), math.exp(-2.0)
+    if same_chunk:
+        want = torch.tensor([e4, e2, 1.0, 0.0], dtype=DT) / (e4 + e2 + 1.0)
+    else:
+        want = torch.tensor([e4, 1.0, 1.0, 0.0], dtype=DT) / (e4 + 2.0)
+    assert torch.allclose(out[0, 0], want.expand(64, 4), rtol=0, atol=1e-15)
+    ob, _ = BF.bf_sparse_piecewise(q[0, 0].numpy(), k[0, 0].numpy(), v[0, 0].numpy(), 0.008,
+                                   order_exact=[[0]], bn=bn)
+    assert np.allclose(ob, want.expand(64, 4).numpy(), atol=1e-15)
+
+
+@pytest.mark.parametrize("bn", [16, 32])
+@pytest.mark.parametrize("nq,nkv,sp,seed", [(2, 70, 0.05, 14), (1, 129, 0.02, 15)])
+def test_sparse_chunk_size_matches_bruteforce_loops(nq, nkv, sp, seed, bn):
+    D = 8
+    q = _randn(1, 1, nq * 64, D, seed=seed)
+    k = _randn(1, 1, nkv * 64, D, seed=seed + 100)
+    v = _randn(1, 1, nkv * 64, D, seed=seed + 200)
+    out, idx, _ = O.sparse_piecewise_attn(q, k, v, sparsity=sp, bn=bn)
+    ob, ib = BF.bf_sparse_piecewise(q[0, 0].numpy(), k[0, 0].numpy(), v[0, 0].numpy(), sp, bn=bn)
+    assert idx[0, 0].tolist() == ib
+    assert np.allclose(out[0, 0].numpy(), ob, rtol=0, atol=1e-12)
+
+
+def test_sparse_chunk_size_irrelevant_when_the_exact_max_dominates():
+    # blockwise-constant inputs keep every interval score below the exact max: the running
+    # max never moves, so every BN gives the same result (and that result is exact)
+    q = _blockwise_constant(3, 8, seed=10)
+    k = _blockwise_constant(70, 8, seed=11)
+    v = _randn(1, 1, 70 * 64, 8, seed=12)
+    outs = [O.sparse_piecewise_attn(q, k, v, sparsity=0.05, bn=bn)[0] for bn in (16, 32, 64)]
+    assert torch.allclose(outs[0], outs[2], rtol=0, atol=1e-13)
+    assert torch.allclose(outs[1], outs[2], rtol=0, atol=1e-13)
+
+
 def test_planted_rescaling_mistake_is_caught():
     """A copy of the interval update that rescales g_acc/g_l disagrees with the oracle on
     the quirk case, so the quirk check above discriminates."""
