@@ -200,11 +200,12 @@ icsa_flash_kernel(FlashParams p) {
   auto soft = [&](int k) {
     const int mask_from = k < p.n_tgt_tiles ? p.t_limit - k * ATT_BN : ATT_BN;
     if (mask_from < ATT_BN) {
+      const int thr = mask_threshold(mask_from, lane);
 #pragma unroll
       for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
         for (int i = 0; i < 16; ++i)
-          if (32 * sub + acc_row(i, lane) >= mask_from) s[sub][i] = -INFINITY;
+          if (acc_row_const(sub, i) >= thr) s[sub][i] = -INFINITY;
     }
     // four partial sums: a single chain of 32 dependent adds measured 0.4 % slower
     float rsv[4];

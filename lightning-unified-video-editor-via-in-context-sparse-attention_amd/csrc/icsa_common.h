@@ -128,6 +128,14 @@ __device__ __forceinline__ int acc_row(int i, int lane) {
   return (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
 }
 
+// Row 32 sub + acc_row(i, lane) of a 64-row tile held as two 32x32 accumulators is at or
+// past `limit` iff the lane-independent part 32 sub + 8 (i / 4) + i % 4 reaches the
+// threshold mask_threshold(limit, lane).  Testing against that threshold compares each
+// element with a compile-time constant: no per-element row values are kept in registers
+// (which the compiler would otherwise rematerialise on every tile, mask or not).
+__device__ __forceinline__ int mask_threshold(int limit, int lane) { return limit - (lane >> 5) * 4; }
+__device__ __forceinline__ constexpr int acc_row_const(int sub, int i) { return 32 * sub + 8 * (i >> 2) + (i & 3); }
+
 // ---------------------------------------------------------------------------------------
 // kernel parameter blocks (passed by value)
 // ---------------------------------------------------------------------------------------

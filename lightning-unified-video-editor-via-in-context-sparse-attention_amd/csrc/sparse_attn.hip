@@ -416,11 +416,12 @@ icsa_sparse_kernel(SparseParams p) {
     const TileRows kv_next = issue_k(t + 1);   // T > T1: always a next K tile
     // keys past Sk take no part (the Triton host; its new KV never straddles)
     if (p.mask_tail && kv_pending.vB < ATT_BN) {
+      const int thr = mask_threshold(kv_pending.vB, lane);
 #pragma unroll
       for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
         for (int i = 0; i < 16; ++i)
-          if (32 * sub + acc_row(i, lane) >= kv_pending.vB) s[sub][i] = -INFINITY;
+          if (acc_row_const(sub, i) >= thr) s[sub][i] = -INFINITY;
     }
     float mx = -INFINITY;
 #pragma unroll

@@ -255,11 +255,12 @@ __global__ void __launch_bounds__(BW_THREADS) icsa_sparse_bwd_dq_kernel(SparseBw
     qk_tile_bw(s, reinterpret_cast<const bf16*>(ks), qf);                  // S^T[key][query]
     qk_tile_bw(dp, reinterpret_cast<const bf16*>(ks + K_TILE_BYTES), dof); // dP^T
     if (t < n_ex) {
+      const int thr = mask_threshold(kvalid, lane);
 #pragma unroll
       for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
-          const bool masked = 32 * sub + acc_row(e, lane) >= kvalid;   // keys past TKV
+          const bool masked = acc_row_const(sub, e) >= thr;           // keys past TKV
           const float pr = masked ? 0.f : __builtin_amdgcn_exp2f(fmaf(s[sub][e], p.scale_log2, -lse));
           dsf[2 * sub + (e >> 3)][e & 7] = (bf16)(pr * (dp[sub][e] - dd));
         }
