@@ -76,9 +76,17 @@
 #define SP_WAIT_ALL() asm volatile("s_waitcnt vmcnt(0)" ::: "memory")
 
 // Real rows of a loaded tile: [0, vA) of the first segment [0, a) and [a, a + vB) of the
-// second; every other row is zeroed after the load (a = 0: rows [0, vB) real).
+// second; every other row is zeroed after the load (a = 0: rows [0, vB) real).  The three
+// counts (each 0 .. 64) are packed into one word: a tile descriptor is live across a whole
+// step, and three of them as separate scalars push the straddling instantiation past its
+// scalar registers (spilled to vector lanes and reloaded in the loop).
 struct TileRows {
-  int a, vA, vB;
+  int w;   // a | vA << 8 | vB << 16
+  __device__ __forceinline__ TileRows() : w(0) {}
+  __device__ __forceinline__ TileRows(int a, int vA, int vB) : w(a | (vA << 8) | (vB << 16)) {}
+  __device__ __forceinline__ int a() const { return w & 0xff; }
+  __device__ __forceinline__ int vA() const { return (w >> 8) & 0xff; }
+  __device__ __forceinline__ int vB() const { return w >> 16; }
 };
 
 template <bool VROW, bool SEG>
@@ -189,23 +197,21 @@ icsa_sparse_kernel(SparseParams p) {
   auto issue_straddle = [&](unsigned char* dst, const bf16* head, int64_t rs_el, int tok_a, int src,
                             bool vrow) -> TileRows {
     const int tok_b = src < 0 ? -1 : ATT_BN * src;
-    TileRows v;
-    v.a = seg_a;
-    v.vA = max(0, min(seg_a, p.Sk - tok_a));
-    v.vB = tok_b < 0 ? 0 : max(0, min(ATT_BN - seg_a, p.Sk - tok_b));
+    const int vA = max(0, min(seg_a, p.Sk - tok_a));
+    const int vB = tok_b < 0 ? 0 : max(0, min(ATT_BN - seg_a, p.Sk - tok_b));
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(head, ((int64_t)(p.Sk - 1) * rs_el + ICSA_D) * 2);
     const int rs2 = (int)rs_el * 2;
 #pragma unroll
     for (int i = 0; i < SP_DMA_PER_TILE; ++i) {
       const int r = k_row0 + 4 * i;
       const bool lo = r < seg_a;
-      const bool ok = lo ? r < v.vA : r - seg_a < v.vB;
+      const bool ok = lo ? r < vA : r - seg_a < vB;
       const int tok = ok ? (lo ? tok_a + r : tok_b + r - seg_a) : 0;
       const int swz = vrow ? rv_swz(r) : (r & 15);
       const int off = tok * rs2 + (((lane & 15) ^ swz) << 4);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)(dst + 1024 * i), 16, off, 0, 0, 0);
     }
-    return v;
+    return TileRows(seg_a, vA, vB);
   };
 
   // Tile g: g < T1 exact block src_l[g]; T1 <= g < T2 pass-1 chunk g - T1 (K only);
@@ -242,7 +248,7 @@ icsa_sparse_kernel(SparseParams p) {
       const int off = r * rs2 + (((lane & 15) ^ (r & 15)) << 4);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)(dst + 1024 * i), 16, off, 0, 0, 0);
     }
-    return TileRows{0, 0, valid};
+    return TileRows(0, 0, valid);
   };
   auto issue_v = [&](int g) -> TileRows {
     const bf16* base;
@@ -288,16 +294,17 @@ icsa_sparse_kernel(SparseParams p) {
       }
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)(dst + 1024 * i), 16, off, 0, 0, 0);
     }
-    return TileRows{0, 0, valid};
+    return TileRows(0, 0, valid);
   };
   // After the wait: zero this wave's key rows that are not real in the K buffer / a V row
   // tile (rows past the sequence and zero blocks are zero keys and values).
   auto fill_rows = [&](unsigned char* buf, TileRows v) {
-    if (v.vA >= v.a && v.vB >= ATT_BN - v.a) return;
+    const int va = v.a(), vA = v.vA(), vB = v.vB();
+    if (vA >= va && vB >= ATT_BN - va) return;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int r = 32 * wave + 4 * i + (lane >> 4);
-      if (r < v.a ? r >= v.vA : r - v.a >= v.vB)   // 4-byte stores: one zero register
+      if (r < va ? r >= vA : r - va >= vB)         // 4-byte stores: one zero register
         for (int e = 0; e < 4; ++e) *reinterpret_cast<unsigned*>(buf + r * ICSA_D * 2 + (lane & 15) * 16 + 4 * e) = 0u;
     }
   };
@@ -306,7 +313,7 @@ icsa_sparse_kernel(SparseParams p) {
     if constexpr (VROW) {
       fill_rows(vbuf, v);
     } else {
-      if (v.vB > 0) return;
+      if (v.vB() > 0) return;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const int d = 64 * wave + 8 * i + (lane >> 3);
@@ -401,7 +408,7 @@ icsa_sparse_kernel(SparseParams p) {
   float l_run = 0.f;
 
   TileRows kv_pending = issue_k(0);
-  TileRows vv_pending{0, 0, 0};
+  TileRows vv_pending;
 
   // ---- 1. exact blocks ----
   // Three barriers per block: V(t) is issued right after the first one, which every wave
@@ -415,8 +422,8 @@ icsa_sparse_kernel(SparseParams p) {
     ATT_BARRIER();                       // K buffer free
     const TileRows kv_next = issue_k(t + 1);   // T > T1: always a next K tile
     // keys past Sk take no part (the Triton host; its new KV never straddles)
-    if (p.mask_tail && kv_pending.vB < ATT_BN) {
-      const int thr = mask_threshold(kv_pending.vB, lane);
+    if (!SEG && p.mask_tail && kv_pending.vB() < ATT_BN) {
+      const int thr = mask_threshold(kv_pending.vB(), lane);
 #pragma unroll
       for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
