@@ -88,9 +88,12 @@ def test_fp32_v(gpu, real, pad):
     _run_case(gpu, q, k, v.float(), t)
 
 
-def test_unaligned_target_and_partial_last_block(gpu):
-    # t % 64 != 0 (new-KV blocks straddle source blocks) and S % 64 != 0
-    q, k, v, t = make_inputs(H=2, real=2000, pad=0, kind="random", seed=4)
+@pytest.mark.parametrize("real", [2000, 2002])
+def test_unaligned_target_and_partial_last_block(gpu, real):
+    # t % 64 != 0 (new-KV blocks straddle source blocks) and S % 64 != 0; t % 64 = 16 puts
+    # the segment boundary of a straddling tile between DMA rows of 4, t % 64 = 18 inside one
+    q, k, v, t = make_inputs(H=2, real=real, pad=0, kind="random", seed=4)
+    assert t % 64 == real % 64
     _run_case(gpu, q, k, v, t)
 
 
