@@ -92,7 +92,9 @@ enum icsa_ws_slot {
   ICSA_WS_VC,         /* bf16 [B*H, NKVp, D] new-KV block sums of v (t % 64 != 0 only) */
   ICSA_WS_COLP,       /* f32 [B*H, ceil(n_t/64), n_s] source-column mass per target strip */
   ICSA_WS_L3S,        /* f32 [B*H, n_diffuse, NKV] level-3 block scores (scratch;    */
-                      /* afterwards its first B*H*8 floats hold the interval bound)  */
+                      /* afterwards its first B*H*8 floats hold the interval bound;  */
+                      /* before them, the compressed stage's split value means,      */
+                      /* bf16 [B*H, 2, D, ceil(NB/64)*64]; sized for the larger)     */
   ICSA_WS_RSTAT,      /* f32 [B*H, NB, 2]   row max and 1 / row sum of the compressed softmax */
   ICSA_WS_COUNT
 };

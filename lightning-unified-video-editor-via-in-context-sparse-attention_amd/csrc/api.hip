@@ -110,7 +110,8 @@ Layout editing_layout(int B, int S, int H, const Sizes& z, int t, int q_dtype, i
   sz[ICSA_WS_L3] = BH * std::max(z.n_diffuse, 1) * z.top_k * 4;
   sz[ICSA_WS_VC] = unaligned ? BH * z.NKVp * D * 2 : 0;
   sz[ICSA_WS_COLP] = BH * ceil_div(z.n_t, ICSA_BLOCK) * std::max(z.n_s, 1) * 4;
-  sz[ICSA_WS_L3S] = BH * std::max(z.n_diffuse, 1) * z.NKV * 4;
+  // the level-3 scores, and before them the compressed stage's split value means
+  sz[ICSA_WS_L3S] = std::max(BH * std::max(z.n_diffuse, 1) * z.NKV * 4, compressed_vmt_bytes((int)BH, z.NB));
   sz[ICSA_WS_RSTAT] = BH * z.NB * 2 * 4;
   Layout L;
   int64_t o = 0;
@@ -293,6 +294,7 @@ int editing_impl(ICSA_EDITING_ARGS, void* const* stage_events, const float* qsum
   cp.sharp = reinterpret_cast<float*>(WS(ICSA_WS_SHARP));
   cp.colpart = reinterpret_cast<float*>(WS(ICSA_WS_COLP));
   cp.rstat = reinterpret_cast<float*>(WS(ICSA_WS_RSTAT));
+  cp.vmt = reinterpret_cast<bf16*>(WS(ICSA_WS_L3S));    // free until the level-3 scores
   cp.BH = BH; cp.NB = z.NB; cp.S = S; cp.n_t = z.n_t; cp.n_s = z.n_s; cp.k_sparsity = z.k_sparsity;
   ICSA_HIP_TRY(launch_compressed(cp, stream), "compressed attention");
   ICSA_HIP_TRY(mark(ICSA_STAGE_COMPRESSED), "event");

@@ -10,6 +10,7 @@
 // Every ranked decision uses the rule "larger value first, lower index first on ties".
 // All score arithmetic is fp32 with fixed reduction orders, so repeated runs are bitwise
 // identical and no float atomics are used.
+#include "attn_tile.h"
 #include "icsa_kernels.h"
 
 #define ICSA_MAX_NB 4096     // longest P row held in registers by the strip kernel
@@ -291,103 +292,208 @@ __global__ void __launch_bounds__(256) icsa_compressed_stats_kernel(CompressedPa
 }
 
 // ---------------------------------------------------------------------------------------
-// (c) one 64-row strip of P per workgroup of 8 waves, in 64-column chunks: P = exp(L - m)/z
-//     formed in LDS (nothing downstream reads P itself, so it is not written back),
-//     out_c += P (Vs/size) with fp32 MFMA (wave w: rows 32 (w & 1), columns 32 (w >> 1)), and
-//     for strips holding target rows the column sums of the source columns over those rows
-//     (partials in strip order, summed by the select kernel).
+// (c) one 64-row strip of P per workgroup of 8 waves, in 32-key chunks: out_c = P Vm with
+//     P = exp(L - m) / z, on the bf16 matrix pipe from split operands.  Per chunk:
+//       * the chunk's logits (64 x 32 fp32) and its split, transposed value means (two bf16
+//         planes of 128 dims x 32 keys, icsa_vmean_split_kernel) arrive by LDS DMA, double
+//         buffered: chunk c + 1 is in flight while chunk c is computed, and two workgroups
+//         share each CU (65 KB of LDS each);
+//       * P is formed once in fp32 and kept as its two bf16 parts P = Ph + Pl (to 2^-17 of
+//         P), and, for strips holding target rows, also in fp32 for the column sums of the
+//         source columns over those rows (rows in order: the strip's partial, summed across
+//         strips by the select kernel);
+//       * wave w adds Pl Vh + Ph Vl + Ph Vh over the chunk's two 16-key steps into output
+//         rows 32 (w % 2) .. + 31, columns 32 (w / 2) .. + 31 (the dropped Pl Vl is below
+//         2^-16 of each product).
+//     Fixed orders throughout, so repeated runs are bitwise identical.
 // ---------------------------------------------------------------------------------------
-__global__ void __launch_bounds__(512) icsa_compressed_rows_kernel(CompressedParams p) {
-  __shared__ float ps[64][68];
-  __shared__ float vs[64][132];
+#define RW_PB_LD 36                             // floats per P row in LDS (16-byte skew)
+
+// Vm = Vsum / block size, transposed and split in two bf16 parts:
+// vmt[((bh * 2 + part) * D + d) * NBp + key], zero for keys >= NB.
+__global__ void __launch_bounds__(256) icsa_vmean_split_kernel(CompressedParams p, int NBp) {
+  __shared__ float tile[64][ICSA_D + 4];
+  const int k0 = blockIdx.x * 64, bh = blockIdx.y;
+  const int NB = p.NB, t = threadIdx.x;
+  const float* V = p.vsum + (int64_t)bh * NB * ICSA_D;
+  floatx4 v[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {                 // float4 f = t + 256 j: key f / 32, dims 4 (f % 32)
+    const int f = t + 256 * j, key = k0 + (f >> 5);
+    v[j] = key < NB ? *reinterpret_cast<const floatx4*>(V + (int64_t)key * ICSA_D + 4 * (f & 31))
+                    : floatx4{0.f, 0.f, 0.f, 0.f};
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int f = t + 256 * j, key = k0 + (f >> 5);
+    if (key < NB) {
+      const float inv = 1.f / block_size_f(key, NB, p.S);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[j][e] *= inv;
+    }
+    *reinterpret_cast<floatx4*>(&tile[f >> 5][4 * (f & 31)]) = v[j];
+  }
+  __syncthreads();
+  const int d = t >> 1, kh = t & 1;             // dim d, keys 32 kh .. + 31
+  bf16* dst = p.vmt + ((int64_t)bh * 2 * ICSA_D + d) * NBp + k0 + 32 * kh;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    bf16x8 hi, lo;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float x = tile[32 * kh + 8 * g + i][d];
+      const bf16 h = f2bf(x);
+      hi[i] = h;
+      lo[i] = f2bf(x - bf2f(h));
+    }
+    *reinterpret_cast<bf16x8*>(dst + 8 * g) = hi;
+    *reinterpret_cast<bf16x8*>(dst + (int64_t)ICSA_D * NBp + 8 * g) = lo;
+  }
+}
+
+// LDS DMA issued from inline assembly: the compiler does not track these loads, so it
+// inserts no waits for them before LDS reads of the other stage; the kernel waits itself
+// (vmcnt(0) before the barrier that opens each chunk).  Lane l of one instruction lands at
+// lds_addr + 16 l.  The resource words are those of make_rsrc (raw buffer, no stride).
+__device__ __forceinline__ u32x4 rw_rsrc(const void* base, int64_t bytes) {
+  const unsigned long long a = (unsigned long long)base;
+  const int n = bytes > 0x7fffffffLL ? 0x7fffffff : (int)(bytes < 0 ? 0 : bytes);
+  u32x4 r;
+  r[0] = (unsigned)__builtin_amdgcn_readfirstlane((int)(unsigned)a);
+  r[1] = (unsigned)__builtin_amdgcn_readfirstlane((int)((unsigned)(a >> 32) & 0xffffu));
+  r[2] = (unsigned)__builtin_amdgcn_readfirstlane(n);
+  r[3] = 0x00020000u;
+  return r;
+}
+__device__ __forceinline__ void rw_dma16(unsigned lds_addr, int voff, u32x4 rs) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :: "s"(lds_addr), "v"(voff), "s"(rs) : "memory", "m0");
+}
+__device__ __forceinline__ unsigned lds_u32(const void* p) {
+  return (unsigned)__builtin_amdgcn_readfirstlane(
+      (int)(unsigned)(size_t)(const __attribute__((address_space(3))) void*)p);
+}
+
+__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4)))
+icsa_compressed_rows_kernel(CompressedParams p, int NBp) {
+  // two stages of the chunk operands as separate objects; 65 KB in all, two workgroups per CU
+  __shared__ __attribute__((aligned(16))) float lc0[64 * 32], lc1[64 * 32];          // logits
+  __shared__ __attribute__((aligned(16))) bf16 vc0[2 * ICSA_D * 32], vc1[2 * ICSA_D * 32];  // Vm^T planes
+  __shared__ __attribute__((aligned(16))) float pb[64 * RW_PB_LD];   // P as [Ph x 8 | Pl x 8] per 8 keys
+  __shared__ __attribute__((aligned(16))) float pf[64 * 32];         // fp32 P (target strips)
   __shared__ float row_m[64], row_iz[64];
   const int strip = blockIdx.x, bh = blockIdx.y;
   const int NB = p.NB, n_t = p.n_t;
   const int r_base = strip * 64;
-  const float* Lbh = p.L + (int64_t)bh * NB * NB;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   if (tid < 64) {
     const int row = r_base + tid;
     row_m[tid] = row < NB ? p.rstat[2 * ((int64_t)bh * NB + row)] : 0.f;
     row_iz[tid] = row < NB ? p.rstat[2 * ((int64_t)bh * NB + row) + 1] : 0.f;
   }
-  const float* V = p.vsum + (int64_t)bh * NB * ICSA_D;
-  const int li = lane & 31, hl = lane >> 5;
-  const int r0 = 32 * (w & 1), c0 = 32 * (w >> 1);
   const int n_ts = (n_t + ICSA_BLOCK - 1) / ICSA_BLOCK;
   const int tgt_rows = min(64, n_t - r_base);          // > 0 only for target strips
-  floatx16 acc = {};
-  // the next chunk's logits (8 per thread: row e / 64, column e % 64 for e = tid + 512 x)
-  // and its V block sums (4 float4 per thread: block kk = e / 32, dims 4 (e % 32)) are
-  // loaded into registers while the current chunk is multiplied
-  float lg[8];
-  floatx4 vv[4];
-  auto load_chunk = [&](int k0) {
+  const int nch = NBp / 32;                            // even
+
+  // DMA sources: the strip's logit rows (rows past NB and keys past the last row are
+  // outside the resource: no load, and P is zero there) and the head's value planes
+  const float* Lbh = p.L + (int64_t)bh * NB * NB;
+  const u32x4 rs_l = rw_rsrc(Lbh + (int64_t)r_base * NB, (int64_t)max(0, min(64, NB - r_base)) * NB * 4);
+  const u32x4 rs_v = rw_rsrc(p.vmt + (int64_t)bh * 2 * ICSA_D * NBp, (int64_t)2 * ICSA_D * NBp * 2);
+  // logits: wave w moves rows 8 w .. + 7 (128 bytes each), 16 bytes per lane
+  const int l_off = ((8 * w + (lane >> 3)) * NB + 4 * (lane & 7)) * 4;
+  // value planes: instruction j (0, 1) of wave w moves rows R = 16 (2 w + j) .. + 15 of the
+  // 256 (plane R / 128, dim R % 128), 64 bytes each; physical 16-byte unit lane % 4 of row R
+  // holds logical unit (lane % 4) ^ (R % 4)
+  int v_off[2];
 #pragma unroll
-    for (int x = 0; x < 8; ++x) {
-      const int e = tid + 512 * x;
-      const int row = r_base + (e >> 6), col = k0 + (e & 63);
-      lg[x] = (row < NB && col < NB) ? Lbh[(int64_t)row * NB + col] : 0.f;
-    }
+  for (int j = 0; j < 2; ++j) {
+    const int R = 16 * (2 * w + j) + (lane >> 2);
+    v_off[j] = ((R >> 7) * ICSA_D + (R & 127)) * NBp * 2 + 16 * ((lane & 3) ^ (R & 3));
+  }
+  auto issue = [&](int c, float* lc, bf16* vc) {
+    rw_dma16(lds_u32(lc + 256 * w), l_off + 128 * c, rs_l);
 #pragma unroll
-    for (int x = 0; x < 4; ++x) {
-      const int e = tid + 512 * x;
-      const int kc = k0 + (e >> 5);
-      vv[x] = kc < NB ? *reinterpret_cast<const floatx4*>(V + (int64_t)kc * ICSA_D + 4 * (e & 31))
-                      : floatx4{0.f, 0.f, 0.f, 0.f};
-    }
+    for (int j = 0; j < 2; ++j) rw_dma16(lds_u32(vc + 512 * (2 * w + j)), v_off[j] + 64 * c, rs_v);
   };
-  __syncthreads();
-  load_chunk(0);
-  for (int k0 = 0; k0 < NB; k0 += 64) {
+
+  const int li = lane & 31, hl = lane >> 5;
+  const int rh = w & 1, dc = 32 * (w >> 1);
+  floatx16 acc = {};
+  // one chunk of 32 keys: P from lc (thread: row t / 8, keys 4 (t % 8) .. + 3), then the
+  // MFMAs on vc
+  auto chunk = [&](int c, const float* lc, const bf16* vc) {
+    const int k0 = 32 * c;
+    const bool want_cs = tgt_rows > 0 && k0 + 32 > n_t;   // uniform
+    {
+      const int r = tid >> 3, q = tid & 7, row = r_base + r;
+      const floatx4 a = *reinterpret_cast<const floatx4*>(lc + r * 32 + 4 * q);
+      const float m = row_m[r], iz = row_iz[r];
+      float pv[4];
+      bf16x4 hi, lo;
 #pragma unroll
-    for (int x = 0; x < 8; ++x) {                     // P = exp(L - m) / z, to LDS only
-      const int e = tid + 512 * x;
-      const int r = e >> 6, kk = e & 63;
-      const int row = r_base + r, col = k0 + kk;
-      const float pv = (row < NB && col < NB) ? expf(lg[x] - row_m[r]) * row_iz[r] : 0.f;
-      ps[r][kk] = pv;
-    }
-#pragma unroll
-    for (int x = 0; x < 4; ++x) {                     // V block means
-      const int e = tid + 512 * x;
-      const int kk = e >> 5, kc = k0 + kk;
-      floatx4 v = vv[x];
-      if (kc < NB) {
-        const float inv = 1.f / block_size_f(kc, NB, p.S);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) v[q] *= inv;
+      for (int i = 0; i < 4; ++i) {
+        const int col = k0 + 4 * q + i;
+        pv[i] = (row < NB && col < NB) ? expf(a[i] - m) * iz : 0.f;
+        const bf16 h = f2bf(pv[i]);
+        hi[i] = h;
+        lo[i] = f2bf(pv[i] - bf2f(h));
       }
-      *reinterpret_cast<floatx4*>(&vs[kk][4 * (e & 31)]) = v;
+      // 8-key group q / 2, half q % 2: Ph at floats 8 (q / 2) + 2 (q % 2), Pl 4 floats on
+      float* dst = pb + r * RW_PB_LD + 8 * (q >> 1) + 2 * (q & 1);
+      *reinterpret_cast<bf16x4*>(dst) = hi;
+      *reinterpret_cast<bf16x4*>(dst + 4) = lo;
+      if (want_cs) *reinterpret_cast<floatx4*>(pf + r * 32 + 4 * q) = floatx4{pv[0], pv[1], pv[2], pv[3]};
     }
-    __syncthreads();
-    if (k0 + 64 < NB) load_chunk(k0 + 64);
-#pragma unroll 2
-    for (int s = 0; s < 32; s += 4) {
-      const floatx4 a = *reinterpret_cast<const floatx4*>(&ps[r0 + li][32 * hl + s]);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) acc = mfma32x32x2f32(a[j], vs[32 * hl + s + j][c0 + li], acc);
-    }
-    if (tgt_rows > 0 && k0 + 64 > n_t && tid < 64) {
+    ATT_BARRIER();                                   // P of the chunk ready
+    if (want_cs && tid < 32) {
       const int col = k0 + tid;
       if (col >= n_t && col < NB) {
         float cs = 0.f;
-        for (int r = 0; r < tgt_rows; ++r) cs += ps[r][tid];
+        for (int r = 0; r < tgt_rows; ++r) cs += pf[r * 32 + tid];
         p.colpart[((int64_t)bh * n_ts + strip) * p.n_s + (col - n_t)] = cs;
       }
     }
-    __syncthreads();
+    const float* prow = pb + (32 * rh + li) * RW_PB_LD;
+    const int d = dc + li;
+    const bf16* vh = vc + d * 32;
+    const bf16* vl = vc + (ICSA_D + d) * 32;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const int u = 2 * s + hl;                      // logical 16-byte unit: keys 8 u .. + 7
+      const bf16x8 ah = *reinterpret_cast<const bf16x8*>(prow + 8 * u);
+      const bf16x8 al = *reinterpret_cast<const bf16x8*>(prow + 8 * u + 4);
+      const int pu = (u ^ (d & 3)) * 8;
+      const bf16x8 bh_ = *reinterpret_cast<const bf16x8*>(vh + pu);
+      const bf16x8 bl_ = *reinterpret_cast<const bf16x8*>(vl + pu);
+      acc = mfma32x32x16(al, bh_, acc);
+      acc = mfma32x32x16(ah, bl_, acc);
+      acc = mfma32x32x16(ah, bh_, acc);
+    }
+  };
+
+  __syncthreads();                                   // row statistics in LDS
+  issue(0, lc0, vc0);
+  for (int c = 0; c < nch; c += 2) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); // chunk c (and this wave's older stores)
+    ATT_BARRIER();                                   // chunk c in LDS; chunk c - 1 consumed
+    issue(c + 1, lc1, vc1);                          // nch is even
+    chunk(c, lc0, vc0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    ATT_BARRIER();
+    if (c + 2 < nch) issue(c + 2, lc0, vc0);
+    chunk(c + 1, lc1, vc1);
   }
   float* out = p.out_c + (int64_t)bh * NB * ICSA_D;
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
-    const int row = r_base + r0 + acc_row(i, lane);
-    if (row < NB) out[(int64_t)row * ICSA_D + c0 + li] = acc[i];
+    const int row = r_base + 32 * rh + acc_row(i, lane);
+    if (row < NB) out[(int64_t)row * ICSA_D + dc + li] = acc[i];
   }
 }
 
 hipError_t launch_compressed(const CompressedParams& p, hipStream_t stream) {
-  if (p.NB > ICSA_MAX_NB) return hipErrorInvalidValue;
+  if (p.NB > ICSA_MAX_NB || p.vmt == nullptr) return hipErrorInvalidValue;
   const int nt = (p.NB + 63) / 64;
   hipLaunchKernelGGL(icsa_compressed_logits_kernel, dim3((p.NB + LG_ROWS - 1) / LG_ROWS, LG_SPLIT, p.BH),
                      dim3(256), 0, stream, p);
@@ -409,7 +515,11 @@ hipError_t launch_compressed(const CompressedParams& p, hipStream_t stream) {
     hipLaunchKernelGGL(icsa_compressed_stats_kernel<64>, sgrid, dim3(256), 0, stream, p);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(icsa_compressed_rows_kernel, dim3(nt, p.BH), dim3(512), 0, stream, p);
+  const int NBp = compressed_nbp(p.NB);
+  hipLaunchKernelGGL(icsa_vmean_split_kernel, dim3(NBp / 64, p.BH), dim3(256), 0, stream, p, NBp);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(icsa_compressed_rows_kernel, dim3(nt, p.BH), dim3(512), 0, stream, p, NBp);
   return hipGetLastError();
 }
 

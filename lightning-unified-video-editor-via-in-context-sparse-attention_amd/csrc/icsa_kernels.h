@@ -33,9 +33,13 @@ struct CompressedParams {
   float* sharp;         // [BH, NB]
   float* colpart;       // [BH, ceil(n_t/64), n_s] source-column sums per 64-row target strip
   float* rstat;         // [BH, NB, 2] row max, 1 / row sum of exp
+  bf16* vmt;            // [BH, 2, D, compressed_nbp(NB)] scratch: the value means transposed,
+                        // split in two bf16 parts (written and read by the compressed stage)
   int BH, NB, S;        // S: tokens (last block size = S - (NB-1)*64)
   int n_t, n_s, k_sparsity;
 };
+inline int compressed_nbp(int NB) { return (NB + 63) / 64 * 64; }
+inline int64_t compressed_vmt_bytes(int BH, int NB) { return (int64_t)BH * 2 * ICSA_D * compressed_nbp(NB) * 2; }
 hipError_t launch_compressed(const CompressedParams& p, hipStream_t stream);
 
 struct SelectParams {
