@@ -618,20 +618,44 @@ hipError_t launch_select(const SelectParams& p, hipStream_t stream) {
 // ---------------------------------------------------------------------------------------
 // (e) sums of the new-KV blocks (fp32 for scoring; bf16 rows / transposed for the kernel)
 // ---------------------------------------------------------------------------------------
+// One workgroup per 16 consecutive new-KV blocks, thread d: dim d of each (the 32 source
+// sums of a thread are requested together).  The 16 blocks' V sums of dim d are one
+// 16-slot group of V^T row d, written as 32 contiguous bytes in kv_slot() order (kv_slot
+// swaps two index bits, so it is its own inverse).
 __global__ void __launch_bounds__(128) icsa_newkv_sums_kernel(NewKvSumsParams p) {
-  const int j = blockIdx.x, bh = blockIdx.y, d = threadIdx.x;
-  if (p.seg_a > 0 && j >= p.seg_from && j < p.NKV) return;   // icsa_newkv_straddle_kernel
-  int src = -1;
-  if (j < p.NKV) src = p.map_identity ? j : p.kvmap[(int64_t)bh * p.NKV + j];
-  float ks = 0.f, vs = 0.f;
-  if (src >= 0) {
-    ks = p.ksum[((int64_t)bh * p.Nsrc + src) * ICSA_D + d];
-    vs = p.vsum[((int64_t)bh * p.Nsrc + src) * ICSA_D + d];
+  const int j0 = 16 * blockIdx.x, bh = blockIdx.y, d = threadIdx.x;
+  float ks[16], vs[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int j = j0 + i;
+    int src = -1;
+    if (j < p.NKV) src = p.map_identity ? j : p.kvmap[(int64_t)bh * p.NKV + j];
+    ks[i] = 0.f;
+    vs[i] = 0.f;
+    if (src >= 0) {
+      ks[i] = p.ksum[((int64_t)bh * p.Nsrc + src) * ICSA_D + d];
+      vs[i] = p.vsum[((int64_t)bh * p.Nsrc + src) * ICSA_D + d];
+    }
   }
-  if (j < p.NKV) p.kc32[((int64_t)bh * p.NKV + j) * ICSA_D + d] = ks;
-  p.kc[((int64_t)bh * p.NKVp + j) * ICSA_D + d] = f2bf(ks);
-  if (p.vct) p.vct[((int64_t)bh * ICSA_D + d) * p.NKVp + (j & ~15) + kv_slot(j & 15)] = f2bf(vs);
-  if (p.vc) p.vc[((int64_t)bh * p.NKVp + j) * ICSA_D + d] = f2bf(vs);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int j = j0 + i;
+    if (p.seg_a > 0 && j >= p.seg_from && j < p.NKV) continue;   // icsa_newkv_straddle_kernel
+    if (j < p.NKV) p.kc32[((int64_t)bh * p.NKV + j) * ICSA_D + d] = ks[i];
+    p.kc[((int64_t)bh * p.NKVp + j) * ICSA_D + d] = f2bf(ks[i]);
+    if (p.vc) p.vc[((int64_t)bh * p.NKVp + j) * ICSA_D + d] = f2bf(vs[i]);
+  }
+  if (p.vct) {                    // no straddling blocks where V^T sums are wanted (seg_a == 0)
+    bf16x8 a, b;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      a[s] = f2bf(vs[kv_slot(s)]);
+      b[s] = f2bf(vs[kv_slot(s + 8)]);
+    }
+    bf16* dst = p.vct + ((int64_t)bh * ICSA_D + d) * p.NKVp + j0;
+    *reinterpret_cast<bf16x8*>(dst) = a;
+    *reinterpret_cast<bf16x8*>(dst + 8) = b;
+  }
 }
 
 // Straddling new-KV block j (the pipeline's new KV when t % 64 != 0; see SparseParams):
@@ -683,7 +707,8 @@ __global__ void __launch_bounds__(128) icsa_newkv_straddle_kernel(NewKvSumsParam
 }
 
 hipError_t launch_newkv_sums(const NewKvSumsParams& p, hipStream_t stream) {
-  hipLaunchKernelGGL(icsa_newkv_sums_kernel, dim3(p.NKVp, p.BH), dim3(128), 0, stream, p);
+  if (p.NKVp % 16 != 0 || (p.vct && p.seg_a > 0)) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(icsa_newkv_sums_kernel, dim3(p.NKVp / 16, p.BH), dim3(128), 0, stream, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || p.seg_a <= 0 || p.seg_from >= p.NKV) return e;
   if (!p.kvmap || !p.k.p || !p.v.p) return hipErrorInvalidValue;
