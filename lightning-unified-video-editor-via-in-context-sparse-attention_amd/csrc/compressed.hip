@@ -15,7 +15,6 @@
 
 #define ICSA_MAX_NB 4096     // longest P row held in registers by the strip kernel
 #define ICSA_MAX_SORT 4096   // longest list ranked by the select kernel
-#define ICSA_L3_ROWS 32      // query blocks per workgroup in the level-3 kernel
 #define ICSA_MAX_NKV 2048    // longest level-3 score row held in registers
 
 __device__ __forceinline__ float block_size_f(int blk, int NB, int S) {
@@ -50,22 +49,39 @@ __device__ __forceinline__ void split3_bf16(float x, bf16& h, bf16& m, bf16& l) 
   l = f2bf(r1 - bf2f(m));
 }
 
-__global__ void __launch_bounds__(256) icsa_compressed_logits_kernel(CompressedParams p) {
+// The same fp32-accurate product for the logits and for the level-3 block scores:
+// C[r][c] = (A_r / sa) . (B_c / sb) / div over D = 128, with A's rows optionally gathered
+// through a list, and sa, sb the block sizes (logits) or 1 (level-3 scores: raw sums).
+struct Split3Gemm {
+  const float* A;           // [BH, a_rows, D]
+  const int* rows;          // output row r reads A row rows[bh * rows_stride + rows_offset + r]
+  int rows_stride, rows_offset, a_rows;
+  int n_rows;               // output rows per head
+  const float* B;           // [BH, n_cols, D]
+  int n_cols;
+  float* C;                 // [BH, n_rows, n_cols]
+  int NB, S;                // block sizes (block_mean)
+  float div;
+};
+
+template <bool BLOCK_MEAN>
+__global__ void __launch_bounds__(256) icsa_split3_gemm_kernel(Split3Gemm g) {
   __shared__ __attribute__((aligned(16))) bf16 ks[2][3][LG_COLS][LG_KST];
   const int rt = blockIdx.x, cs = blockIdx.y, bh = blockIdx.z;
-  const int NB = p.NB;
+  const int NC = g.n_cols;
   const int tid = threadIdx.x, w = tid >> 6, l = tid & 63;
   const int li = l & 31, hl = l >> 5;
-  const float* qbase = p.qsum + (int64_t)bh * NB * ICSA_D;
-  const float* kbase = p.ksum + (int64_t)bh * NB * ICSA_D;
+  const float* qbase = g.A + (int64_t)bh * g.a_rows * ICSA_D;
+  const float* kbase = g.B + (int64_t)bh * NC * ICSA_D;
 
-  // A operands: this lane's query row, divided by the block size, split in three parts
+  // A operands: this lane's row (divided by its block size for the logits), split in three
   bf16x8 ah[8], am[8], al[8];
   {
-    const int row = rt * LG_ROWS + 32 * w + li;
-    const bool ok = row < NB;
-    const float sz = ok ? block_size_f(row, NB, p.S) : 1.f;
-    const float* src = qbase + (int64_t)(ok ? row : 0) * ICSA_D + 8 * hl;
+    const int r = rt * LG_ROWS + 32 * w + li;
+    const bool ok = r < g.n_rows;
+    const int row = !ok ? 0 : (g.rows ? g.rows[(int64_t)bh * g.rows_stride + g.rows_offset + r] : r);
+    const float sz = (BLOCK_MEAN && ok) ? block_size_f(row, g.NB, g.S) : 1.f;
+    const float* src = qbase + (int64_t)row * ICSA_D + 8 * hl;
 #pragma unroll
     for (int st = 0; st < 8; ++st) {
       floatx4 v0 = {0.f, 0.f, 0.f, 0.f}, v1 = v0;
@@ -76,7 +92,8 @@ __global__ void __launch_bounds__(256) icsa_compressed_logits_kernel(CompressedP
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         bf16 h, m, lo;
-        split3_bf16((e < 4 ? v0[e] : v1[e - 4]) / sz, h, m, lo);
+        const float x = e < 4 ? v0[e] : v1[e - 4];
+        split3_bf16(BLOCK_MEAN ? x / sz : x, h, m, lo);
         ah[st][e] = h;
         am[st][e] = m;
         al[st][e] = lo;
@@ -84,7 +101,7 @@ __global__ void __launch_bounds__(256) icsa_compressed_logits_kernel(CompressedP
     }
   }
 
-  const int n_ct = (NB + LG_COLS - 1) / LG_COLS;
+  const int n_ct = (NC + LG_COLS - 1) / LG_COLS;
   const int per = (n_ct + LG_SPLIT - 1) / LG_SPLIT;
   const int t0 = cs * per, t1 = min(n_ct, t0 + per);
   if (t0 >= t1) return;                                // uniform for the workgroup
@@ -94,14 +111,16 @@ __global__ void __launch_bounds__(256) icsa_compressed_logits_kernel(CompressedP
   floatx4 pre[4];
   auto load_tile = [&](int t) {
     const int col = t * LG_COLS + kc;
-    if (col < NB) {
-      const float sz = block_size_f(col, NB, p.S);
+    if (col < NC) {
+      const float sz = BLOCK_MEAN ? block_size_f(col, g.NB, g.S) : 1.f;
       const float* src = kbase + (int64_t)col * ICSA_D + kd;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         pre[q] = *reinterpret_cast<const floatx4*>(src + 4 * q);
+        if (BLOCK_MEAN) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) pre[q][e] = pre[q][e] / sz;
+          for (int e = 0; e < 4; ++e) pre[q][e] = pre[q][e] / sz;
+        }
       }
     } else {
 #pragma unroll
@@ -126,8 +145,7 @@ __global__ void __launch_bounds__(256) icsa_compressed_logits_kernel(CompressedP
     }
   };
 
-  const float sq = sqrtf((float)ICSA_D);
-  float* out = p.L + (int64_t)bh * NB * NB;
+  float* out = g.C + (int64_t)bh * g.n_rows * NC;
   load_tile(t0);
   store_tile(0);
   __syncthreads();
@@ -149,11 +167,11 @@ __global__ void __launch_bounds__(256) icsa_compressed_logits_kernel(CompressedP
       acc = mfma32x32x16(ah[st], bh, acc);
     }
     const int col = t * LG_COLS + li;
-    if (col < NB) {
+    if (col < NC) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int row = rt * LG_ROWS + 32 * w + acc_row(i, l);
-        if (row < NB) out[(int64_t)row * NB + col] = acc[i] / sq;
+        if (row < g.n_rows) out[(int64_t)row * NC + col] = acc[i] / g.div;
       }
     }
     if (more) store_tile(buf ^ 1);                     // that buffer was read in step t - 1
@@ -495,8 +513,12 @@ icsa_compressed_rows_kernel(CompressedParams p, int NBp) {
 hipError_t launch_compressed(const CompressedParams& p, hipStream_t stream) {
   if (p.NB > ICSA_MAX_NB || p.vmt == nullptr) return hipErrorInvalidValue;
   const int nt = (p.NB + 63) / 64;
-  hipLaunchKernelGGL(icsa_compressed_logits_kernel, dim3((p.NB + LG_ROWS - 1) / LG_ROWS, LG_SPLIT, p.BH),
-                     dim3(256), 0, stream, p);
+  Split3Gemm g;
+  g.A = p.qsum; g.rows = nullptr; g.rows_stride = 0; g.rows_offset = 0; g.a_rows = p.NB;
+  g.n_rows = p.NB; g.B = p.ksum; g.n_cols = p.NB; g.C = p.L; g.NB = p.NB; g.S = p.S;
+  g.div = sqrtf((float)ICSA_D);
+  hipLaunchKernelGGL(icsa_split3_gemm_kernel<true>, dim3((p.NB + LG_ROWS - 1) / LG_ROWS, LG_SPLIT, p.BH),
+                     dim3(256), 0, stream, g);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int64_t rows = (int64_t)p.BH * p.NB;
@@ -723,67 +745,11 @@ hipError_t launch_newkv_sums(const NewKvSumsParams& p, hipStream_t stream) {
 
 // ---------------------------------------------------------------------------------------
 // (f) level-3: per query block, top_k new-KV blocks by QCsum . KCsum (fp32), ascending list.
-//     Scores: 32 query blocks per workgroup, fp32 MFMA over 64-block chunks, written to a
-//     scratch row per query block.  Selection: one wave per query block, bisection over the
-//     float keys (ballot counts), then compaction in ascending block order.
+//     Scores: the fp32-accurate split-bf16 product of (a) on the raw sums (128 query blocks
+//     of the list per workgroup, a quarter of the new-KV blocks), written to a scratch row
+//     per query block.  Selection: one wave per query block, bisection over the float keys
+//     (ballot counts), then compaction in ascending block order.
 // ---------------------------------------------------------------------------------------
-__global__ void __launch_bounds__(128) icsa_level3_scores_kernel(Level3Params p) {
-  __shared__ float qs[ICSA_L3_ROWS][132];
-  __shared__ float ks[64][132];
-  const int bh = blockIdx.y;
-  const int r_base = blockIdx.x * ICSA_L3_ROWS;
-  const int NKV = p.NKV;
-  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int li = lane & 31, hl = lane >> 5;
-  for (int e = threadIdx.x; e < ICSA_L3_ROWS * 32; e += 128) {
-    const int r = e >> 5, c4 = e & 31;
-    floatx4 qv = {0.f, 0.f, 0.f, 0.f};
-    if (r_base + r < p.n_rows) {
-      const int qb = p.rows ? p.rows[(int64_t)bh * p.rows_stride + p.rows_offset + r_base + r] : r_base + r;
-      qv = *reinterpret_cast<const floatx4*>(p.qsum + ((int64_t)bh * p.NQsrc + qb) * ICSA_D + 4 * c4);
-    }
-    *reinterpret_cast<floatx4*>(&qs[r][4 * c4]) = qv;
-  }
-  const float* kc = p.kc32 + (int64_t)bh * NKV * ICSA_D;
-  float* sc = p.scores + ((int64_t)bh * p.n_rows + r_base) * NKV;
-  // the next chunk's 64 rows are loaded into registers (16 float4 per thread) while the
-  // current chunk is multiplied
-  floatx4 kpre[16];
-  auto load_chunk = [&](int k0) {
-#pragma unroll
-    for (int x = 0; x < 16; ++x) {
-      const int e = threadIdx.x + 128 * x, r = e >> 5, c4 = e & 31;
-      kpre[x] = k0 + r < NKV ? *reinterpret_cast<const floatx4*>(kc + (int64_t)(k0 + r) * ICSA_D + 4 * c4)
-                             : floatx4{0.f, 0.f, 0.f, 0.f};
-    }
-  };
-  load_chunk(0);
-  for (int k0 = 0; k0 < NKV; k0 += 64) {
-    __syncthreads();                              // q rows ready / previous chunk consumed
-#pragma unroll
-    for (int x = 0; x < 16; ++x) {
-      const int e = threadIdx.x + 128 * x, r = e >> 5, c4 = e & 31;
-      *reinterpret_cast<floatx4*>(&ks[r][4 * c4]) = kpre[x];
-    }
-    __syncthreads();
-    if (k0 + 64 < NKV) load_chunk(k0 + 64);
-    floatx16 acc = {};
-#pragma unroll 4
-    for (int kk = 0; kk < 64; kk += 4) {
-      const floatx4 a = *reinterpret_cast<const floatx4*>(&qs[li][64 * hl + kk]);
-      const floatx4 b = *reinterpret_cast<const floatx4*>(&ks[32 * w + li][64 * hl + kk]);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) acc = mfma32x32x2f32(a[j], b[j], acc);
-    }
-    const int blk = k0 + 32 * w + li;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int row = acc_row(i, lane);
-      if (r_base + row < p.n_rows && blk < NKV) sc[(int64_t)row * NKV + blk] = acc[i];
-    }
-  }
-}
-
 template <int VPL>   // scores per lane: NKV <= 64 * VPL
 __global__ void __launch_bounds__(256) icsa_level3_select_kernel(Level3Params p) {
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -833,8 +799,12 @@ __global__ void __launch_bounds__(256) icsa_level3_select_kernel(Level3Params p)
 hipError_t launch_level3(const Level3Params& p, hipStream_t stream) {
   if (p.NKV > ICSA_MAX_NKV || p.top_k > p.NKV || p.top_k < 1) return hipErrorInvalidValue;
   if (p.n_rows <= 0) return hipSuccess;
-  hipLaunchKernelGGL(icsa_level3_scores_kernel, dim3((p.n_rows + ICSA_L3_ROWS - 1) / ICSA_L3_ROWS, p.BH),
-                     dim3(128), 0, stream, p);
+  Split3Gemm g;
+  g.A = p.qsum; g.rows = p.rows; g.rows_stride = p.rows_stride; g.rows_offset = p.rows_offset;
+  g.a_rows = p.NQsrc; g.n_rows = p.n_rows; g.B = p.kc32; g.n_cols = p.NKV; g.C = p.scores;
+  g.NB = 0; g.S = 0; g.div = 1.f;
+  hipLaunchKernelGGL(icsa_split3_gemm_kernel<false>, dim3((p.n_rows + LG_ROWS - 1) / LG_ROWS, LG_SPLIT, p.BH),
+                     dim3(256), 0, stream, g);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int64_t rows = (int64_t)p.BH * p.n_rows;
