@@ -68,7 +68,7 @@
 #define SP_PF 2                          // MFMA operand read-ahead (steps); 3 or 4 measured no faster
 #define SP_DMA_PER_TILE 8                // LDS-DMA instructions per wave per K or V tile
 #ifndef SP_SWEEP_CONC
-#define SP_SWEEP_CONC 256                // sweep start advances NKV / SP_SWEEP_CONC per launch
+#define SP_SWEEP_CONC 128                // sweep start advances NKV / SP_SWEEP_CONC per launch
 #endif
 
 // vmcnt waits: "all but the newest tile" / "everything".  Loads complete in issue order.
