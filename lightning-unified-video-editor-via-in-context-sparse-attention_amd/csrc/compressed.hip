@@ -37,7 +37,7 @@ __device__ __forceinline__ float block_size_f(int blk, int NB, int S) {
 //     into registers while the current one is multiplied.  A fixed order of MFMAs, so
 //     repeated runs are bitwise identical.
 // ---------------------------------------------------------------------------------------
-#define LG_SPLIT 4
+#define LG_SPLIT 3
 #define LG_ROWS 128
 #define LG_COLS 32
 #define LG_KST 136            // bf16 row stride of a split K tile (272 B: conflict-free reads)
@@ -746,7 +746,7 @@ hipError_t launch_newkv_sums(const NewKvSumsParams& p, hipStream_t stream) {
 // ---------------------------------------------------------------------------------------
 // (f) level-3: per query block, top_k new-KV blocks by QCsum . KCsum (fp32), ascending list.
 //     Scores: the fp32-accurate split-bf16 product of (a) on the raw sums (128 query blocks
-//     of the list per workgroup, a quarter of the new-KV blocks), written to a scratch row
+//     of the list per workgroup, a third of the new-KV blocks), written to a scratch row
 //     per query block.  Selection: one wave per query block, bisection over the float keys
 //     (ballot counts), then compaction in ascending block order.
 // ---------------------------------------------------------------------------------------
