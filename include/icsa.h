@@ -165,7 +165,8 @@ int icsa_editing_sparse_attention_ev(
 
 /* icsa_editing_sparse_attention without a workspace argument and without any allocation:
  * its scratch is a file-scope __device__ array of ICSA_NOALLOC_SCRATCH_BYTES, one per
- * device, which the device holds until the process ends.  Same arguments (minus
+ * device, which the device holds from this entry's first call on it until the process
+ * ends (the array's code object loads at that call).  Same arguments (minus
  * workspace / workspace_bytes), semantics and results as icsa_editing_sparse_attention.
  * Calls whose workspace (icsa_editing_workspace_size) exceeds the scratch return
  * ICSA_EUNSUPPORTED before any device work; 256 MiB covers, e.g., B = 1, S = 65,536,

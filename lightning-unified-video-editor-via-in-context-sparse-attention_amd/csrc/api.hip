@@ -436,9 +436,12 @@ int icsa_editing_sparse_attention_presummed(ICSA_EDITING_ARGS, void* const* stag
 
 // ---------------------------------------------------------------------------------------
 // No-allocation variant of icsa_editing_sparse_attention: its workspace is this file-scope
-// device array (each device that runs the library holds its own copy until the process
-// ends).  In host code `scratch` names a host-side stand-in, never the device memory, so
-// the host only ever uses the per-device address returned by hipGetSymbolAddress.
+// device array (each device on which the entry runs holds its own copy until the process
+// ends).  This file defines no kernel, so the array's code object is loaded onto a device
+// only by the hipGetSymbolAddress of the entry's first call there; keep kernels out of this
+// file, or every process that launches them would hold the array.  In host code `scratch`
+// names a host-side stand-in, never the device memory, so the host only ever uses the
+// per-device address returned by hipGetSymbolAddress.
 // ---------------------------------------------------------------------------------------
 static __device__ __align__(256) unsigned char scratch[ICSA_NOALLOC_SCRATCH_BYTES];
 
