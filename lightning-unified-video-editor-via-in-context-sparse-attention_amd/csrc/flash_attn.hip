@@ -173,23 +173,25 @@ icsa_flash_kernel(FlashParams p) {
   unsigned char* dma_dst = smem;
   bool dma_on = false;
   // sets up this wave's part of tile j: K(j) for group 1, V^T(j) for group 0
+  // Byte ranges fit 32 bits (checked at launch), so only the base addresses take 64-bit
+  // arithmetic: the setup runs in the SOFT phase, where its scalar work competes with the
+  // exponentials.  Past the last tile the issue stays branch-free: an empty range into a
+  // junk LDS area.
+  const int k_row_bytes = (int)p.k_ss * 2;
+  const int v_rec = (ICSA_D - 1) * (int)p.vt_sd * 2 + ATT_BN * 2;
   auto dma_setup = [&](int j) {
     dma_on = j < n_tiles;
-    if (!dma_on) {                        // issue stays branch-free: an empty range, junk LDS
-      dma_rs = make_rsrc(kb, 0);
-      dma_dst = smem + FA_JUNK_OFF;
-      return;
-    }
-    const int tok0 = tile_tok0(j);
+    const int tok0 = dma_on ? tile_tok0(j) : 0;
     if (lag_w) {
-      const int k_valid = min(ATT_BN, p.Sk - tok0);
-      const int64_t k_bytes = k_valid > 0 ? ((int64_t)(k_valid - 1) * p.k_ss + ICSA_D) * 2 : 0;
-      dma_rs = make_rsrc(kb + (int64_t)tok0 * p.k_ss, k_bytes);
-      dma_dst = kbuf(j) + dw * 4096;
+      const int k_valid = dma_on ? min(ATT_BN, p.Sk - tok0) : 0;
+      const int k_rec = k_valid > 0 ? (k_valid - 1) * k_row_bytes + ICSA_D * 2 : 0;
+      dma_rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16*>(kb + (int64_t)tok0 * p.k_ss), (short)0, k_rec,
+                                                 0x00020000);
     } else {
-      dma_rs = make_rsrc(vb + (int64_t)j * ATT_BN, ((int64_t)(ICSA_D - 1) * p.vt_sd + ATT_BN) * 2);
-      dma_dst = vbuf(j) + dw * 4096;
+      dma_rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16*>(vb + (int64_t)(dma_on ? j : 0) * ATT_BN),
+                                                 (short)0, dma_on ? v_rec : 0, 0x00020000);
     }
+    dma_dst = !dma_on ? smem + FA_JUNK_OFF : (lag_w ? kbuf(j) : vbuf(j)) + dw * 4096;
   };
   auto dma_seg = [&](int i) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(dma_rs, (lds_ptr)(dma_dst + 1024 * i), 16, dofs[i], 0, 0, 0);
@@ -200,12 +202,21 @@ icsa_flash_kernel(FlashParams p) {
   auto soft = [&](int k) {
     const int mask_from = k < p.n_tgt_tiles ? p.t_limit - k * ATT_BN : ATT_BN;
     if (mask_from < ATT_BN) {
-      const int thr = mask_threshold(mask_from, lane);
+      // keys >= mask_from as one 64-bit word; element i of sub-tile sub is key
+      // 32 sub + 8 (i / 4) + 4 hl + i % 4, bit 8 (i / 4) + i % 4 of word sub of the word
+      // shifted by 4 hl.  Integer selects: per-element compares would hold 32 lane masks in
+      // scalar registers, which spill into vector lanes and slow every SOFT phase.
+      const unsigned long long mw = (~0ull << max(mask_from, 0)) >> (4 * hl);
 #pragma unroll
-      for (int sub = 0; sub < 2; ++sub)
+      for (int sub = 0; sub < 2; ++sub) {
+        const unsigned wd = (unsigned)(mw >> (32 * sub));
 #pragma unroll
-        for (int i = 0; i < 16; ++i)
-          if (acc_row_const(sub, i) >= thr) s[sub][i] = -INFINITY;
+        for (int i = 0; i < 16; ++i) {
+          const int kb = 8 * (i >> 2) + (i & 3);
+          const unsigned all = (unsigned)((int)(wd << (31 - kb)) >> 31);
+          s[sub][i] = __uint_as_float((all & 0xff800000u) | (__float_as_uint(s[sub][i]) & ~all));
+        }
+      }
     }
     // four partial sums: a single chain of 32 dependent adds measured 0.4 % slower
     float rsv[4];
