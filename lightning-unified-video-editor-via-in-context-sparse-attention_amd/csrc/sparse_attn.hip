@@ -189,6 +189,13 @@ icsa_sparse_kernel(SparseParams p) {
   // list entry of exact tile g (the ascending list rotated to start at entry rot)
   auto ex_entry = [&](int g) -> int { return g + rot < top_k ? g + rot : g + rot - top_k; };
 
+  // Buffer resources with 32-bit byte ranges (every per-(b, h) slice fits: checked at
+  // launch), so only the base addresses take 64-bit arithmetic: the scalar setup of a tile
+  // runs once per step beside the softmax, and spilled scalar registers cost vector lanes.
+  auto rsrc32 = [](const void* base, int bytes) -> __amdgpu_buffer_rsrc_t {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
+  };
+
   // A straddling exact tile (tokA_l >= 0): rows r < seg_a from token tok_a + r, rows
   // r >= seg_a from token 64 src + r - seg_a.  One buffer resource over the head's rows,
   // per-lane row offsets; rows past Sk (or of a zero block) read token 0 and are zeroed
@@ -199,8 +206,8 @@ icsa_sparse_kernel(SparseParams p) {
     const int tok_b = src < 0 ? -1 : ATT_BN * src;
     const int vA = max(0, min(seg_a, p.Sk - tok_a));
     const int vB = tok_b < 0 ? 0 : max(0, min(ATT_BN - seg_a, p.Sk - tok_b));
-    const __amdgpu_buffer_rsrc_t rs = make_rsrc(head, ((int64_t)(p.Sk - 1) * rs_el + ICSA_D) * 2);
     const int rs2 = (int)rs_el * 2;
+    const __amdgpu_buffer_rsrc_t rs = rsrc32(head, (p.Sk - 1) * rs2 + ICSA_D * 2);
 #pragma unroll
     for (int i = 0; i < SP_DMA_PER_TILE; ++i) {
       const int r = k_row0 + 4 * i;
@@ -220,7 +227,7 @@ icsa_sparse_kernel(SparseParams p) {
   // padded -- or a zero block).
   auto issue_k = [&](int g) -> TileRows {
     const bf16* base;
-    int64_t bytes;
+    int bytes;
     int valid, rs2;                        // rs2: key row stride in bytes
     const bool ex = g < T1;
     if (ex) {
@@ -231,16 +238,16 @@ icsa_sparse_kernel(SparseParams p) {
       const int tok0 = src * ATT_BN;
       valid = src < 0 ? 0 : min(ATT_BN, p.Sk - tok0);
       base = kbase + (src < 0 ? 0 : (int64_t)tok0 * p.k_st);
-      bytes = valid > 0 ? ((int64_t)(valid - 1) * p.k_st + ICSA_D) * 2 : 0;
       rs2 = (int)p.k_st * 2;
+      bytes = valid > 0 ? (valid - 1) * rs2 + ICSA_D * 2 : 0;
     } else {
       const int c = g < T2 ? g - T1 : g - T2;
       valid = ATT_BN;
       base = kcb + (int64_t)c * ATT_BN * ICSA_D;
-      bytes = (int64_t)ATT_BN * ICSA_D * 2;
+      bytes = ATT_BN * ICSA_D * 2;
       rs2 = ICSA_D * 2;
     }
-    const __amdgpu_buffer_rsrc_t rs = make_rsrc(base, bytes);
+    const __amdgpu_buffer_rsrc_t rs = rsrc32(base, bytes);
     unsigned char* dst = kbuf + wave * 8192;
 #pragma unroll
     for (int i = 0; i < SP_DMA_PER_TILE; ++i) {
@@ -252,7 +259,7 @@ icsa_sparse_kernel(SparseParams p) {
   };
   auto issue_v = [&](int g) -> TileRows {
     const bf16* base;
-    int64_t bytes;
+    int bytes;
     int valid, rs2;                        // rs2: row stride in bytes (V rows / V^T d rows)
     const bool ex = g < T1;
     if (ex) {
@@ -264,23 +271,23 @@ icsa_sparse_kernel(SparseParams p) {
           if (tok_a >= 0) return issue_straddle(vbuf + wave * 8192, vbase, p.v_st, tok_a, src, true);
         valid = src < 0 ? 0 : min(ATT_BN, p.Sk - tok0);
         base = vbase + (src < 0 ? 0 : (int64_t)tok0 * p.v_st);
-        bytes = valid > 0 ? ((int64_t)(valid - 1) * p.v_st + ICSA_D) * 2 : 0;
         rs2 = (int)p.v_st * 2;
+        bytes = valid > 0 ? (valid - 1) * rs2 + ICSA_D * 2 : 0;
       } else {                           // V^T holds new-KV block j at columns 64 j ..
         const int jn = __builtin_amdgcn_readfirstlane(nkv_l[ex_entry(g)]);
         valid = jn < 0 ? 0 : ATT_BN;
         base = vbase + (jn < 0 ? 0 : (int64_t)jn * ATT_BN);
-        bytes = jn < 0 ? 0 : ((int64_t)(ICSA_D - 1) * p.vt_sd + ATT_BN) * 2;
         rs2 = (int)p.vt_sd * 2;
+        bytes = jn < 0 ? 0 : (ICSA_D - 1) * rs2 + ATT_BN * 2;
       }
     } else {
       const int c = g - T2;
       valid = ATT_BN;
       base = vcb + (int64_t)c * ATT_BN * (VROW ? ICSA_D : 1);
-      bytes = VROW ? (int64_t)ATT_BN * ICSA_D * 2 : ((int64_t)(ICSA_D - 1) * p.NKVp + ATT_BN) * 2;
       rs2 = VROW ? ICSA_D * 2 : p.NKVp * 2;
+      bytes = VROW ? ATT_BN * ICSA_D * 2 : (ICSA_D - 1) * rs2 + ATT_BN * 2;
     }
-    const __amdgpu_buffer_rsrc_t rs = make_rsrc(base, bytes);
+    const __amdgpu_buffer_rsrc_t rs = rsrc32(base, bytes);
     unsigned char* dst = vbuf + wave * 8192;
 #pragma unroll
     for (int i = 0; i < SP_DMA_PER_TILE; ++i) {
@@ -423,12 +430,19 @@ icsa_sparse_kernel(SparseParams p) {
     const TileRows kv_next = issue_k(t + 1);   // T > T1: always a next K tile
     // keys past Sk take no part (the Triton host; its new KV never straddles)
     if (!SEG && p.mask_tail && kv_pending.vB() < ATT_BN) {
-      const int thr = mask_threshold(kv_pending.vB(), lane);
+      // keys >= vB as one 64-bit word; element i of sub-tile sub is key 32 sub + 8 (i / 4) +
+      // 4 hl + i % 4: integer selects, no per-element compare masks in scalar registers
+      const unsigned long long mw = (~0ull << kv_pending.vB()) >> (4 * hl);
 #pragma unroll
-      for (int sub = 0; sub < 2; ++sub)
+      for (int sub = 0; sub < 2; ++sub) {
+        const unsigned wd = (unsigned)(mw >> (32 * sub));
 #pragma unroll
-        for (int i = 0; i < 16; ++i)
-          if (acc_row_const(sub, i) >= thr) s[sub][i] = -INFINITY;
+        for (int i = 0; i < 16; ++i) {
+          const int kb = 8 * (i >> 2) + (i & 3);
+          const unsigned all = (unsigned)((int)(wd << (31 - kb)) >> 31);
+          s[sub][i] = __uint_as_float((all & 0xff800000u) | (__float_as_uint(s[sub][i]) & ~all));
+        }
+      }
     }
     float mx = -INFINITY;
 #pragma unroll
