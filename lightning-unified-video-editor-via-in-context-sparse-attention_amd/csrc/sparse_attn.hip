@@ -195,13 +195,16 @@ icsa_sparse_kernel(SparseParams p) {
   auto rsrc32 = [](const void* base, int bytes) -> __amdgpu_buffer_rsrc_t {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
   };
+  // element strides as 32-bit values: launch_sparse rejects slices with Sk * stride * 2 at or
+  // above 2^31, so every token offset tok * stride inside a (b, h) slice fits 32 bits
+  const int k_st32 = (int)p.k_st, v_st32 = (int)p.v_st;
 
   // A straddling exact tile (tokA_l >= 0): rows r < seg_a from token tok_a + r, rows
   // r >= seg_a from token 64 src + r - seg_a.  One buffer resource over the head's rows,
   // per-lane row offsets; rows past Sk (or of a zero block) read token 0 and are zeroed
   // after the wait.  Returns the rows that are real: [0, vA) and [seg_a, seg_a + vB).
   const int seg_a = p.seg_a;
-  auto issue_straddle = [&](unsigned char* dst, const bf16* head, int64_t rs_el, int tok_a, int src,
+  auto issue_straddle = [&](unsigned char* dst, const bf16* head, int rs_el, int tok_a, int src,
                             bool vrow) -> TileRows {
     const int tok_b = src < 0 ? -1 : ATT_BN * src;
     const int vA = max(0, min(seg_a, p.Sk - tok_a));
@@ -234,11 +237,11 @@ icsa_sparse_kernel(SparseParams p) {
       const int tok_a = __builtin_amdgcn_readfirstlane(tokA_l[ex_entry(g)]);
       const int src = __builtin_amdgcn_readfirstlane(src_l[ex_entry(g)]);
       if constexpr (SEG)
-        if (tok_a >= 0) return issue_straddle(kbuf + wave * 8192, kbase, p.k_st, tok_a, src, false);
+        if (tok_a >= 0) return issue_straddle(kbuf + wave * 8192, kbase, k_st32, tok_a, src, false);
       const int tok0 = src * ATT_BN;
       valid = src < 0 ? 0 : min(ATT_BN, p.Sk - tok0);
-      base = kbase + (src < 0 ? 0 : (int64_t)tok0 * p.k_st);
-      rs2 = (int)p.k_st * 2;
+      base = kbase + (src < 0 ? 0 : tok0 * k_st32);
+      rs2 = k_st32 * 2;
       bytes = valid > 0 ? (valid - 1) * rs2 + ICSA_D * 2 : 0;
     } else {
       const int c = g < T2 ? g - T1 : g - T2;
@@ -268,10 +271,10 @@ icsa_sparse_kernel(SparseParams p) {
       if constexpr (VROW) {
         const int tok_a = __builtin_amdgcn_readfirstlane(tokA_l[ex_entry(g)]);
         if constexpr (SEG)
-          if (tok_a >= 0) return issue_straddle(vbuf + wave * 8192, vbase, p.v_st, tok_a, src, true);
+          if (tok_a >= 0) return issue_straddle(vbuf + wave * 8192, vbase, v_st32, tok_a, src, true);
         valid = src < 0 ? 0 : min(ATT_BN, p.Sk - tok0);
-        base = vbase + (src < 0 ? 0 : (int64_t)tok0 * p.v_st);
-        rs2 = (int)p.v_st * 2;
+        base = vbase + (src < 0 ? 0 : tok0 * v_st32);
+        rs2 = v_st32 * 2;
         bytes = valid > 0 ? (valid - 1) * rs2 + ICSA_D * 2 : 0;
       } else {                           // V^T holds new-KV block j at columns 64 j ..
         const int jn = __builtin_amdgcn_readfirstlane(nkv_l[ex_entry(g)]);
