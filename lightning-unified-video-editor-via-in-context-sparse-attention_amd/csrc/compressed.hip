@@ -220,6 +220,9 @@ __device__ __forceinline__ float wave_sum_dpp(float x) {
 __device__ __forceinline__ uint32_t wave_min_u32(uint32_t x) {
   return wave_reduce(x, 0xffffffffu, [](uint32_t a, uint32_t b) { return a < b ? a : b; });
 }
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t x) {
+  return wave_reduce(x, 0u, [](uint32_t a, uint32_t b) { return a > b ? a : b; });
+}
 
 // Largest key lo with count(key >= lo) >= k over the wave's keys (keys 0 = absent; requires
 // at least k nonzero keys): the key of the k-th largest.  Only registers u < nu can hold
@@ -227,11 +230,23 @@ __device__ __forceinline__ uint32_t wave_min_u32(uint32_t x) {
 // zero keys of a partly used group never count).  Bisection over the key range; as soon
 // as a midpoint has exactly k keys at or above it, the answer is the smallest of those
 // keys (one wave minimum), which for spread-out values ends the search long before the
-// 32nd step.
+// 32nd step.  The search starts from a bracket that the keys themselves give: every lane's
+// largest key is at or above the smallest of the 64 lane maxima, so for k <= 64 that
+// minimum has at least k keys at or above it, and no key lies above the wave's largest.
+// The answer is the same key from any valid bracket; the narrower one saves steps.
 template <int VPL>
 __device__ __forceinline__ uint32_t kth_largest_key(const uint32_t (&key)[VPL], int k, int nu) {
   static_assert(VPL % 4 == 0, "registers are visited in groups of four");
-  uint32_t lo = 0u, hi = 0xffffffffu;
+  uint32_t lmax = 0u;
+#pragma unroll
+  for (int g = 0; g < VPL; g += 4)
+    if (g < nu) {
+#pragma unroll
+      for (int u = g; u < g + 4; ++u) lmax = key[u] > lmax ? key[u] : lmax;
+    }
+  const uint32_t kmax = wave_max_u32(lmax);
+  uint32_t lo = k <= 64 ? wave_min_u32(lmax) : 0u;
+  uint32_t hi = kmax == 0xffffffffu ? kmax : kmax + 1u;
   while (hi - lo > 1u) {
     const uint32_t mid = lo + ((hi - lo) >> 1);
     int c = 0;
